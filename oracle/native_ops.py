@@ -1,0 +1,342 @@
+"""fp64 references and ensemble tolerances of the three pack operators.
+
+Follows vladmt06/kernelverify ``kernelverify/schemas/native_ops.py``:
+``K_QUANT``/``K_NATIVE``/``_EPS``/``_base_tol`` :37-50, the artefact memo and
+``qmm_reference``/``qmm_tolerance`` :87-132, ``_moe_route``/``_moe_combine``/
+``moe_reference``/``MOE_MEMBERS``/``moe_tolerance`` :193-252,
+``_kv_dequant64``/``kv_reference``/``_kv_member``/``KV_MEMBERS``/
+``kv_tolerance`` :293-394, and the ``NATIVE_OPS`` registry :397-404.
+
+Additions the BASELINE configs need and the reference does not carry
+(``qmm_*_artefact`` take a drawn artefact instead of raw weights, config 1's
+"q ~ U{0..15}" case) keep the reference's formulas unchanged: the artefact
+entry points run the same ``r_contract`` and the same six members.
+
+Memory: the serial KV members evaluate per head, which is exact (the
+reductions run along DH or T inside one (b, h) row), so long-context cases
+stay within a few hundred MB.
+
+Parity: the reference functions are pinned by the golden records
+(``quant_device_adequacy.json``: ``ref_scale``/``base_tol``) for the qmm path,
+by the reference's own known-answer tests for moe routing, and by the KV
+invariants (batch-row independence, new-entry dominance, T=1, padded prefix,
+GQA = tiled cache) for the KV path, plus a torch fp64
+``scaled_dot_product_attention`` cross-check of ``kv_reference``.
+"""
+
+from __future__ import annotations
+
+import weakref
+from dataclasses import dataclass
+from typing import Callable
+
+import numpy as np
+
+from oracle.floor import floored_tolerance
+from oracle.native_kernels import _cache_dequant, _topk_by_prob, moe_dispatch, TOP_K
+from oracle.quant_contract import (
+    ENSEMBLE as QUANT_ENSEMBLE,
+    QuantContract,
+    canonical_quantize,
+    r_contract,
+)
+
+K_QUANT = 4.0
+K_NATIVE = 1.5
+
+_EPS = {"float16": 9.77e-4, "float32": 1.19e-7}
+
+
+def _base_tol(dtype: str, ref: np.ndarray) -> float:
+    peak = float(np.max(np.abs(ref))) if ref.size else 0.0
+    return 4.0 * _EPS[dtype] * peak
+
+
+@dataclass(frozen=True)
+class NativeOp:
+    meta: dict
+    reference: Callable
+    tolerance: Callable
+    augment: Callable | None = None
+
+
+# ---------------------------------------------------------------------------
+# quantized_matmul
+# ---------------------------------------------------------------------------
+QUANTIZED_MATMUL_META = {
+    "op_schema": {
+        "inputs": [{"name": "x", "dims": ["B", "D_IN"]},
+                   {"name": "w", "dims": ["D_OUT", "D_IN"]}],
+        "dims": [{"name": "B", "candidates": [1, 4]},
+                 {"name": "D_IN", "candidates": [128, 448, 1024]},
+                 {"name": "D_OUT", "candidates": [16, 512]},
+                 {"name": "BITS", "candidates": [2, 3, 4, 8]}],
+    },
+    "dtypes": ["float32", "float16"],
+    "tolerances": {"float32": 1e-3, "float16": 1e-2},
+}
+
+# One-slot memo keyed by the identity of a live weight matrix: the reference
+# and the tolerance both derive the artefact from the raw weights.
+_qmm_slot: tuple | None = None
+
+
+def _drop_qmm_slot(_ref):
+    global _qmm_slot
+    _qmm_slot = None
+
+
+def _qmm_artefact(inputs):
+    global _qmm_slot
+    w, bits = inputs["w"], int(inputs["bits"][0])
+    if _qmm_slot is not None and _qmm_slot[0]() is w and _qmm_slot[1] == bits:
+        return _qmm_slot[2]
+    art = canonical_quantize(w, QuantContract(bits=bits, group_size=64))
+    _qmm_slot = (weakref.ref(w, _drop_qmm_slot), bits, art)
+    return art
+
+
+def qmm_reference(inputs) -> np.ndarray:
+    return r_contract(inputs["x"], _qmm_artefact(inputs))
+
+
+def qmm_tolerance(case, inputs, ref) -> float:
+    art = _qmm_artefact(inputs)
+    return qmm_tolerance_artefact(case.dtype, inputs["x"], art, ref)
+
+
+def qmm_reference_artefact(x, art) -> np.ndarray:
+    """``r_contract`` on a given artefact (config 1's directly drawn codes)."""
+    return r_contract(x, art)
+
+
+def qmm_tolerance_artefact(dtype: str, x, art, ref) -> float:
+    return floored_tolerance(_base_tol(dtype, ref), K_QUANT,
+                             (fn(x, art) for fn in QUANT_ENSEMBLE.values()), ref)
+
+
+WEIGHT_SCALE = 0.05
+
+
+def _rescaled(arr, target_peak):
+    peak = float(np.max(np.abs(arr.astype(np.float32)))) if arr.size else 0.0
+    if peak == 0.0:
+        return arr
+    return (arr.astype(np.float32) * (target_peak / peak)).astype(arr.dtype)
+
+
+def _as_weights(arr):
+    return _rescaled(arr, WEIGHT_SCALE)
+
+
+def qmm_augment(case, inputs):
+    inputs["bits"] = np.array([case.dim_map["BITS"]], dtype=np.int32)
+    inputs["w"] = _as_weights(inputs["w"])
+    return inputs
+
+
+def moe_augment(case, inputs):
+    inputs["router"] = _as_weights(inputs["router"])
+    inputs["experts"] = _as_weights(inputs["experts"])
+    return inputs
+
+
+# ---------------------------------------------------------------------------
+# moe_dispatch (single linear expert per slot, the reference's contract)
+# ---------------------------------------------------------------------------
+MOE_DISPATCH_META = {
+    "op_schema": {
+        "inputs": [{"name": "x", "dims": ["B", "D"]},
+                   {"name": "router", "dims": ["E", "D"]},
+                   {"name": "experts", "dims": ["E", "D_OUT", "D"]}],
+        "dims": [{"name": "B", "candidates": [1, 8]},
+                 {"name": "D", "candidates": [64, 100, 512]},
+                 {"name": "E", "candidates": [4, 16]},
+                 {"name": "D_OUT", "candidates": [32, 256]}],
+    },
+    "dtypes": ["float32", "float16"],
+    "tolerances": {"float32": 1e-3, "float16": 1e-2},
+}
+
+
+def route_probs(logits: np.ndarray, k: int, dtype):
+    """softmax over every expert, top-k by probability (ties low), renormalised:
+    returns (top indices, renormalised weights) at ``dtype``."""
+    logits = logits.astype(dtype)
+    probs = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    probs /= probs.sum(axis=-1, keepdims=True)
+    top = _topk_by_prob(probs, k, tie_high=False)
+    weights = np.take_along_axis(probs, top, axis=-1)
+    return top, weights / weights.sum(axis=-1, keepdims=True)
+
+
+def _moe_route(inputs, dtype, k=TOP_K):
+    x = inputs["x"].astype(dtype)
+    if "logits" in inputs:
+        top, weights = route_probs(inputs["logits"], k, dtype)
+    else:
+        top, weights = route_probs(x @ inputs["router"].astype(dtype).T, k, dtype)
+    return x, top, weights
+
+
+def _moe_combine(x, experts, top, weights, slots, dtype):
+    """weight * (x @ expert^T), accumulated per row over ``slots`` in order."""
+    out = np.zeros((x.shape[0], experts.shape[1]), dtype=dtype)
+    for row in range(x.shape[0]):
+        for slot in slots:
+            out[row] += weights[row, slot] * (x[row] @ experts[int(top[row, slot])].T)
+    return out
+
+
+def moe_reference(inputs, k=TOP_K) -> np.ndarray:
+    x, top, weights = _moe_route(inputs, np.float64, k)
+    return _moe_combine(x, inputs["experts"].astype(np.float64), top, weights,
+                        range(k), np.float64)
+
+
+def _moe_member_reversed(inputs, k=TOP_K) -> np.ndarray:
+    x, top, weights = _moe_route(inputs, np.float32, k)
+    out = _moe_combine(x, inputs["experts"].astype(np.float32), top, weights,
+                       range(k - 1, -1, -1), np.float32)
+    return out.astype(inputs["x"].dtype)
+
+
+def _moe_member_default(inputs, k=TOP_K) -> np.ndarray:
+    if "logits" in inputs:
+        x, top, weights = _moe_route(inputs, np.float32, k)
+        out = _moe_combine(x, inputs["experts"].astype(np.float32), top, weights,
+                           range(k), np.float32)
+        return out.astype(inputs["x"].dtype)
+    return moe_dispatch(inputs, k=k)
+
+
+MOE_MEMBERS = {
+    "moe:default": _moe_member_default,
+    "moe:reversed-slots": _moe_member_reversed,
+}
+MOE_ENSEMBLE_VERSION = "moe-ensemble-v1"
+
+
+def moe_tolerance(case, inputs, ref, k=TOP_K) -> float:
+    return floored_tolerance(_base_tol(case.dtype, ref), K_NATIVE,
+                             (fn(inputs, k) for fn in MOE_MEMBERS.values()), ref)
+
+
+# ---------------------------------------------------------------------------
+# kv_attention
+# ---------------------------------------------------------------------------
+KV_ATTENTION_META = {
+    "op_schema": {
+        "inputs": [{"name": "q", "dims": ["B", "H", "DH"]},
+                   {"name": "k_cache", "dims": ["H", "T", "DH"]},
+                   {"name": "v_cache", "dims": ["H", "T", "DH"]},
+                   {"name": "new_k", "dims": ["B", "H", "DH"]},
+                   {"name": "new_v", "dims": ["B", "H", "DH"]}],
+        "dims": [{"name": "B", "candidates": [1, 4]},
+                 {"name": "H", "candidates": [2, 8]},
+                 {"name": "T", "candidates": [64, 512]},
+                 {"name": "DH", "candidates": [64, 128]},
+                 {"name": "BITS", "candidates": [4, 8]}],
+    },
+    "dtypes": ["float32", "float16"],
+    "tolerances": {"float32": 1e-3, "float16": 1e-2},
+}
+
+QUERY_SCALE = 0.6
+
+
+def kv_augment(case, inputs):
+    inputs["bits"] = np.array([case.dim_map["BITS"]], dtype=np.int32)
+    inputs["q"] = _rescaled(inputs["q"], QUERY_SCALE)
+    inputs["new_k"] = _rescaled(inputs["new_k"], QUERY_SCALE)
+    return inputs
+
+
+# Two-slot identity memo: one case's k and v caches, dequantized once for the
+# reference and all four members.
+_kv_slots: dict = {}
+
+
+def _kv_dequant64(cache, bits):
+    key = (id(cache), int(bits))
+    hit = _kv_slots.get(key)
+    if hit is not None and hit[0] is cache:
+        return hit[1]
+    if len(_kv_slots) >= 2:
+        _kv_slots.clear()
+    value = _cache_dequant(cache, bits).astype(np.float64)
+    _kv_slots[key] = (cache, value)
+    return value
+
+
+def kv_reference(inputs) -> np.ndarray:
+    """fp64 truth: dequantized canonical caches, the new entry at full
+    precision, softmax over T+1."""
+    q = inputs["q"].astype(np.float64)
+    bits = int(inputs["bits"][0])
+    kd = _kv_dequant64(inputs["k_cache"], bits)
+    vd = _kv_dequant64(inputs["v_cache"], bits)
+    scale = 1.0 / np.sqrt(float(q.shape[-1]))
+    scores = np.einsum("bhd,htd->bht", q, kd) * scale
+    s_new = np.sum(q * inputs["new_k"].astype(np.float64), axis=-1) * scale
+    scores = np.concatenate([scores, s_new[..., None]], axis=-1)
+    probs = np.exp(scores - scores.max(axis=-1, keepdims=True))
+    probs /= probs.sum(axis=-1, keepdims=True)
+    out = np.einsum("bht,htd->bhd", probs[..., :-1], vd)
+    return out + probs[..., -1][..., None] * inputs["new_v"].astype(np.float64)
+
+
+def _kv_member(inputs, *, scores_order="pairwise", combine_order="pairwise"):
+    """fp32 evaluation; the serial orders accumulate with np.add.accumulate
+    (along DH for scores, along T for the combine), evaluated head by head."""
+    q = inputs["q"].astype(np.float32)
+    bits = int(inputs["bits"][0])
+    kd = _kv_dequant64(inputs["k_cache"], bits).astype(np.float32)
+    vd = _kv_dequant64(inputs["v_cache"], bits).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(float(q.shape[-1])))
+    if scores_order == "serial":
+        scores = np.empty(q.shape[:2] + (kd.shape[1],), dtype=np.float32)
+        for h in range(q.shape[1]):
+            prods = q[:, h, None, :] * kd[None, h]
+            scores[:, h] = np.add.accumulate(prods, axis=-1, dtype=np.float32)[..., -1]
+        scores = scores * scale
+    else:
+        scores = np.einsum("bhd,htd->bht", q, kd) * scale
+    s_new = np.sum(q * inputs["new_k"].astype(np.float32), axis=-1) * scale
+    scores = np.concatenate([scores, s_new[..., None]], axis=-1)
+    probs = np.exp(scores - scores.max(axis=-1, keepdims=True))
+    probs /= probs.sum(axis=-1, keepdims=True)
+    pc = probs[..., :-1]
+    if combine_order in ("serial", "reversed"):
+        out = np.empty(q.shape, dtype=np.float32)
+        for h in range(q.shape[1]):
+            contrib = pc[:, h, :, None] * vd[None, h]
+            if combine_order == "reversed":
+                contrib = contrib[:, ::-1, :]
+            out[:, h] = np.add.accumulate(contrib, axis=1, dtype=np.float32)[:, -1]
+    else:
+        out = np.einsum("bht,htd->bhd", pc, vd)
+    out = out + probs[..., -1][..., None] * inputs["new_v"].astype(np.float32)
+    return out.astype(inputs["q"].dtype)
+
+
+KV_MEMBERS = {
+    "kv:pairwise-pairwise": dict(scores_order="pairwise", combine_order="pairwise"),
+    "kv:serial-scores": dict(scores_order="serial", combine_order="pairwise"),
+    "kv:serial-combine": dict(scores_order="pairwise", combine_order="serial"),
+    "kv:reversed-combine": dict(scores_order="pairwise", combine_order="reversed"),
+}
+KV_ENSEMBLE_VERSION = "kv-ensemble-v1"
+
+
+def kv_tolerance(case, inputs, ref) -> float:
+    """K_QUANT borrowed, as in the reference (uncalibrated for this operator)."""
+    return floored_tolerance(_base_tol(case.dtype, ref), K_QUANT,
+                             (_kv_member(inputs, **kw) for kw in KV_MEMBERS.values()), ref)
+
+
+NATIVE_OPS = {
+    "quantized_matmul": NativeOp(QUANTIZED_MATMUL_META, qmm_reference, qmm_tolerance, qmm_augment),
+    "moe_dispatch": NativeOp(MOE_DISPATCH_META, moe_reference, moe_tolerance, moe_augment),
+    "kv_attention": NativeOp(KV_ATTENTION_META, kv_reference, kv_tolerance, kv_augment),
+}
