@@ -1,0 +1,232 @@
+"""Bench the quantized decode pack on one MI355X; prints ONE JSON line.
+
+Workload of ``value`` (the metric's headline case):
+4-bit affine qmv, W 14336 x 4096, group 64, batch M = 1, fp16 x and out.
+A "step" is one ``kvp_qmv`` launch over one weight artefact.
+
+Protocol (kernelverify bench/interleave.py:38-103, bench/pack_wide_qmv.py:282-329,
+re-targeted to HIP):
+- verify first: the GPU output of every timed configuration is checked
+  against the CPU baseline's output on the same inputs before any timing
+  (the CPU leg doubles as the checker; no timing is printed for a failing
+  configuration);
+- weights rotate over >= 1 GiB of distinct artefact copies, more than the
+  256 MB Infinity Cache, so every launch reads HBM;
+- W warmup launches, then EXACTLY K launches back-to-back on one stream,
+  bracketed by device synchronisation, timed by HIP events recorded on that
+  stream; ms_per_step = elapsed / K;
+- ``roofline.achieved`` = algorithmic bytes per launch / ms_per_step, with
+  the bytes of ``kernelverify_amd.pack.wide_qmv.algorithmic_bytes``.
+
+The secondary configurations (8-bit, M = 4/8, 4096 x 14336, KV decode, MoE)
+are reported under "secondary" in the same line.
+
+``--gpus N`` with N > 1 exits: this build measures one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+ROTATION_BYTES = 1 << 30
+METRIC = "achieved HBM GB/s (% of 8 TB/s) + µs/call, 4-bit qmv & quant-KV decode attn"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# qmv workload
+# ---------------------------------------------------------------------------
+class QmvWorkload:
+    def __init__(self, d_out, d_in, bits, m, seed=0):
+        from kernelverify_amd.hip import DeviceArray
+        from kernelverify_amd.pack import wide_qmv
+        from kernelverify_amd.pack.codes import pack_codes
+
+        self.d_out, self.d_in, self.bits, self.m = d_out, d_in, bits, m
+        self.name = f"qmv {bits}b {d_out}x{d_in} M{m}"
+        rng = np.random.default_rng(seed)
+        self.q = rng.integers(0, 1 << bits, size=(d_out, d_in), dtype=np.int32)
+        g = d_in // 64
+        self.scales = np.abs(rng.standard_normal((d_out, g)) * 0.02).astype(np.float16)
+        self.biases = (rng.standard_normal((d_out, g)) * 0.01).astype(np.float16)
+        self.x = rng.standard_normal((m, d_in)).astype(np.float16)
+        self.w_q = pack_codes(self.q, bits)
+        self.bytes = wide_qmv.algorithmic_bytes(m, d_out, d_in, bits)
+        art = wide_qmv.artefact_bytes(d_out, d_in, bits)
+        copies = max(2, -(-ROTATION_BYTES // art))
+        self.dx = DeviceArray.from_host(self.x)
+        self.copies = []
+        for _ in range(copies):
+            self.copies.append((DeviceArray.from_host(self.w_q), DeviceArray.from_host(self.scales),
+                                DeviceArray.from_host(self.biases)))
+        self.out = DeviceArray((m, d_out), np.float16)
+        self._run = wide_qmv.run_qmv
+        self.i = 0
+
+    def step(self, stream):
+        w, s, b = self.copies[self.i % len(self.copies)]
+        self.i += 1
+        self._run(self.dx, w, s, b, self.out, bits=self.bits, stream=stream)
+
+    def gpu_output(self):
+        from kernelverify_amd import hip
+
+        self.step(None)
+        hip.synchronize()
+        return self.out.to_host()
+
+    def cpu_reference(self):
+        """The reference CPU path on this artefact: fp32 dequant then BLAS
+        (kernelverify/reference/native_kernels.py:66-83)."""
+        from oracle.extensions import artefact_from_arrays
+        from oracle.native_kernels import quantized_matmul_artefact
+
+        art = artefact_from_arrays(self.q, self.scales, self.biases, self.bits)
+        return lambda: quantized_matmul_artefact(self.x, art)
+
+
+def time_steps(workload, steps: int, warmup: int):
+    from kernelverify_amd import hip
+
+    stream = hip.Stream()
+    for _ in range(warmup):
+        workload.step(stream)
+    hip.synchronize()
+    start, stop = hip.Event(), hip.Event()
+    start.record(stream)
+    for _ in range(steps):
+        workload.step(stream)
+    stop.record(stream)
+    stop.synchronize()
+    hip.synchronize()
+    return start.elapsed_ms(stop) / steps
+
+
+def cpu_baseline(fn, budget_s: float = 12.0, min_reps: int = 3):
+    """Best and median wall time of the CPU path over a bounded sample."""
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return min(times), float(np.median(times)), len(times)
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        info = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        return int(info[0]["num_threads"]) if info else 1
+    except Exception:
+        return int(os.environ.get("OMP_NUM_THREADS", "1"))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--secondary", action="store_true", help="also time the secondary configs")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
+              "(every GPU box has one MI355X; the multi-GPU sharding is a design note)",
+              file=sys.stderr)
+        return 2
+
+    from kernelverify_amd import hip, lib
+
+    if hip.device_count() == 0:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 3
+    lib.load()
+
+    head = QmvWorkload(14336, 4096, 4, 1)
+    log(f"[bench] {head.name}: {len(head.copies)} artefact copies, "
+        f"{head.bytes} algorithmic bytes/launch")
+
+    # Verify first: GPU output against the CPU path on the same inputs.
+    got = head.gpu_output()
+    ref_fn = head.cpu_reference()
+    ref = ref_fn()
+    err = float(np.max(np.abs(got.astype(np.float64) - ref.astype(np.float64))))
+    tol = 4 * 9.77e-4 * float(np.max(np.abs(ref.astype(np.float64))))
+    log(f"[bench] verify {head.name}: max|gpu-cpu| {err:.3e} (bound {tol:.3e})")
+    if not err <= tol:
+        print(f"bench.py: verification failed for {head.name}", file=sys.stderr)
+        return 1
+
+    ms = time_steps(head, args.steps, args.warmup)
+    us = ms * 1e3
+    gbs = head.bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] {head.name}: {us:.3f} us/call, {gbs:.1f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)")
+
+    secondary = []
+    if args.secondary:
+        for d_out, d_in, bits, m in ((4096, 4096, 4, 1), (14336, 4096, 8, 1), (14336, 4096, 4, 4),
+                                     (14336, 4096, 4, 8), (4096, 14336, 4, 1)):
+            w = QmvWorkload(d_out, d_in, bits, m, seed=1)
+            g = w.gpu_output()
+            r = w.cpu_reference()()
+            e = float(np.max(np.abs(g.astype(np.float64) - r)))
+            t = 4 * 9.77e-4 * float(np.max(np.abs(r)))
+            if not e <= t:
+                log(f"[bench] verify FAILED {w.name}: {e:.3e} > {t:.3e}")
+                continue
+            ms2 = time_steps(w, max(200, args.steps // 2), args.warmup)
+            secondary.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3),
+                              "GBps": round(w.bytes / (ms2 * 1e-3) / 1e9, 1),
+                              "frac_8TBps": round(w.bytes / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+            log(f"[bench] {secondary[-1]}")
+            del w
+
+    cpu = None
+    if not args.no_cpu:
+        best, med, n = cpu_baseline(ref_fn)
+        cpu = {"value": round(head.bytes / best / 1e9, 3), "unit": "GB/s",
+               "cores": blas_threads(), "kind": "port",
+               "sample": f"{n} calls of the numpy control path (fp32 dequant + BLAS sgemv, "
+                         f"native_kernels.py:66-83) on the same 14336x4096 4-bit artefact; "
+                         f"best {best * 1e3:.1f} ms, median {med * 1e3:.1f} ms; "
+                         f"host {platform.processor() or platform.machine()}, "
+                         f"os.cpu_count()={os.cpu_count()}"}
+        log(f"[bench] cpu baseline: {cpu}")
+
+    line = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "us_per_call": round(us, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u4 codes x f16 -> f32 accumulate",
+        "data": "synthetic (BASELINE configs[1] distributions, seed 0)",
+        "config": {"workload": head.name, "d_out": 14336, "d_in": 4096, "bits": 4, "group": 64,
+                   "batch": 1, "rotation_copies": len(head.copies)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    if secondary:
+        line["secondary"] = secondary
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,49 @@
+"""The C-ABI library: it loads, and exports every entry point the header declares.
+
+No compute call here: this runs without a GPU.
+"""
+
+import re
+from pathlib import Path
+
+import pytest
+
+from kernelverify_amd import lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "kvpack.h"
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(kvp_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_pack():
+    names = declared_symbols()
+    for must in ("kvp_qmv", "kvp_kv_decode", "kvp_moe_route", "kvp_moe_permute",
+                 "kvp_moe_dispatch", "kvp_moe_swiglu", "kvp_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    cdll = lib.load()
+    missing = [n for n in declared_symbols() if not hasattr(cdll, n)]
+    assert not missing, missing
+
+
+def test_binding_table_matches_header():
+    assert sorted(lib.SIGNATURES) == declared_symbols()
+
+
+def test_version_names_the_target():
+    assert "gfx950" in lib.version()
+
+
+def test_argument_errors_are_statuses_not_crashes():
+    """Argument checks run on the host before anything touches a device."""
+    cdll = lib.load()
+    rc = cdll.kvp_qmv(None, None, None, None, None, lib.KVP_F16, 1, 16, 64, 4, None)
+    assert rc == lib.KVP_INVALID
+    assert "null pointer" in lib.last_error()
+    with pytest.raises(lib.InvalidArgument):
+        lib.check(rc)
