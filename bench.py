@@ -75,13 +75,13 @@ class QmvWorkload:
             self.copies.append((DeviceArray.from_host(self.w_q), DeviceArray.from_host(self.scales),
                                 DeviceArray.from_host(self.biases)))
         self.out = DeviceArray((m, d_out), np.float16)
-        self._run = wide_qmv.run_qmv
+        self.calls = [wide_qmv.QmvCall(self.dx, w, s, b, self.out, bits=bits)
+                      for w, s, b in self.copies]
         self.i = 0
 
     def step(self, stream):
-        w, s, b = self.copies[self.i % len(self.copies)]
+        self.calls[self.i % len(self.calls)](stream)
         self.i += 1
-        self._run(self.dx, w, s, b, self.out, bits=self.bits, stream=stream)
 
     def gpu_output(self):
         from kernelverify_amd import hip
@@ -100,20 +100,39 @@ class QmvWorkload:
         return lambda: quantized_matmul_artefact(self.x, art)
 
 
-def time_steps(workload, steps: int, warmup: int):
+def time_steps(workload, steps: int, warmup: int, graph: bool = True):
+    """ms per step over EXACTLY ``steps`` back-to-back launches.
+
+    With ``graph`` the launches are captured once into a HIP graph and
+    replayed, so the host's per-launch cost (ctypes, Python) cannot starve
+    the GPU: the figure is the device's own time per call, as a serving loop
+    that replays a captured decode step sees it. Without it, every launch is
+    a host call (the eager figure, reported beside it).
+    """
     from kernelverify_amd import hip
 
     stream = hip.Stream()
     for _ in range(warmup):
         workload.step(stream)
     hip.synchronize()
+    g = None
+    if graph:
+        g = hip.Graph(stream, lambda: [workload.step(stream) for _ in range(steps)])
+        g.launch()  # the replay itself warmed once
+        stream.synchronize()
+    hip.synchronize()
     start, stop = hip.Event(), hip.Event()
     start.record(stream)
-    for _ in range(steps):
-        workload.step(stream)
+    if g is not None:
+        g.launch()
+    else:
+        for _ in range(steps):
+            workload.step(stream)
     stop.record(stream)
     stop.synchronize()
     hip.synchronize()
+    if g is not None:
+        g.destroy()
     return start.elapsed_ms(stop) / steps
 
 

@@ -71,6 +71,10 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Compiler-only barrier: keeps LDS reads of one unrolled step from being
+// hoisted above the previous step's math (bounds live registers at wide M).
+__device__ __forceinline__ void sched_fence() { asm volatile("" ::: "memory"); }
+
 // Non-temporal 16-byte load for streamed-once data (weights, cache pages):
 // it should not evict the activations other waves still need from L2.
 __device__ __forceinline__ u32x4 load_stream16(const uint32_t* p) {

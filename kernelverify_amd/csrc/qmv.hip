@@ -21,6 +21,8 @@
 //     narrower than fp32 except the fp16 inputs themselves (contract C1).
 //   * Activations larger than the LDS budget are staged in block-uniform
 //     chunks of whole 64-unit lane rounds.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace kvp {
@@ -28,6 +30,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kUPL = 2;  // units per lane per pipeline step
 // LDS budget for staged activations, in 32-bit words (fp16 pairs), per block.
 constexpr int kStageWords = 16384;  // 64 KiB: two blocks fit in a CU's 160 KiB
 
@@ -40,17 +43,21 @@ struct Geom {
   static constexpr int kUnitPairs = kUnitCodes / 2;          // staged x words per unit
   static constexpr int kCodesPerWord = 32 / BITS;            // 2/4/8-bit only
   static constexpr int kPairsPerWord = kCodesPerWord / 2;
+  // LDS slots of a unit: one per weight word (its pairs contiguous), or one
+  // per code pair for 3-bit. Slot-major layout [m][slot][unit][pairs] keeps a
+  // wave's 64 lanes on consecutive addresses for every read.
+  static constexpr int kSlots = kMagic ? kUnitWords : kUnitPairs;
+  static constexpr int kSlotPairs = kMagic ? kPairsPerWord : 1;
 };
 
 template <int BITS>
-__device__ __forceinline__ void load_unit(const uint32_t* p, uint32_t (&w)[Geom<BITS>::kUnitWords]) {
+__device__ __forceinline__ void load_unit(const uint32_t* p, uint32_t* w) {
   if constexpr (Geom<BITS>::kUnitWords == 4) {
     u32x4 v = load_stream16(p);
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
   } else {
-    // 24-byte unit, 8-byte aligned.
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < 3; ++i) {  // 24-byte unit, 8-byte aligned
       u32x2 v = load_stream8(p + 2 * i);
       w[2 * i] = v.x;
       w[2 * i + 1] = v.y;
@@ -71,9 +78,12 @@ __device__ __forceinline__ void load_unit(const uint32_t* p, uint32_t (&w)[Geom<
 // the word, (n2,n6), (16 n3, 16 n7) from the word shifted by 8: one shift,
 // four ANDs and four dot2 per eight codes. The x pairs staged for this word
 // are (x0,x4), (x1,x5), (x2,x6), (x3,x7).
+//
+// `xu` points at slot 0 of this unit for m = 0; slot j of activation row m
+// is at xu + (m * kSlots + j) * slot_stride (in words).
 template <int BITS, int M, int RW>
 __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUnitWords],
-                                         const uint32_t* __restrict__ xu, int m_stride,
+                                         const uint32_t* __restrict__ xu, int slot_stride,
                                          float (&d)[RW][M]) {
   using G = Geom<BITS>;
   constexpr float kDenormScale = 16777216.0f;  // 2^24
@@ -85,11 +95,10 @@ __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUn
       for (int m = 0; m < M; ++m) d1[r][m] = d16[r][m] = 0.0f;
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi) {
-      uint32_t xp[M][4];
+      u32x4 xp[M];
 #pragma unroll
       for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xp[m][i] = xu[m * m_stride + wi * 4 + i];
+        xp[m] = *reinterpret_cast<const u32x4*>(xu + (m * G::kSlots + wi) * slot_stride);
 #pragma unroll
       for (int r = 0; r < RW; ++r) {
         const uint32_t v = w[r][wi];
@@ -98,12 +107,13 @@ __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUn
         const uint32_t c = v8 & 0x000F000Fu, e = v8 & 0x00F000F0u;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          d1[r][m] = dot2(xp[m][0], a, d1[r][m]);
-          d16[r][m] = dot2(xp[m][1], b, d16[r][m]);
-          d1[r][m] = dot2(xp[m][2], c, d1[r][m]);
-          d16[r][m] = dot2(xp[m][3], e, d16[r][m]);
+          d1[r][m] = dot2(xp[m].x, a, d1[r][m]);
+          d16[r][m] = dot2(xp[m].y, b, d16[r][m]);
+          d1[r][m] = dot2(xp[m].z, c, d1[r][m]);
+          d16[r][m] = dot2(xp[m].w, e, d16[r][m]);
         }
       }
+      if constexpr (M > 4) sched_fence();
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r)
@@ -117,20 +127,53 @@ __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUn
       for (int m = 0; m < M; ++m) d[r][m] = 0.0f;
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi) {
-      uint32_t xp[M][2];
+      u32x2 xp[M];
 #pragma unroll
       for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int i = 0; i < 2; ++i) xp[m][i] = xu[m * m_stride + wi * 2 + i];
+        xp[m] = *reinterpret_cast<const u32x2*>(xu + (m * G::kSlots + wi) * slot_stride);
 #pragma unroll
       for (int r = 0; r < RW; ++r) {
         const uint32_t v = w[r][wi];
         const uint32_t a = v & 0x00FF00FFu, b = (v >> 8) & 0x00FF00FFu;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          d[r][m] = dot2(xp[m][0], a, d[r][m]);
-          d[r][m] = dot2(xp[m][1], b, d[r][m]);
+          d[r][m] = dot2(xp[m].x, a, d[r][m]);
+          d[r][m] = dot2(xp[m].y, b, d[r][m]);
         }
+      }
+      if constexpr (M > 4) sched_fence();
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) d[r][m] *= kDenormScale;
+  } else if constexpr (BITS == 2) {
+    // Pair i of a word = codes (i, i+8), field (w >> 2i) & 0x00030003.
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) d[r][m] = 0.0f;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4 xp[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          xp[m] = *reinterpret_cast<const u32x4*>(xu + (m * G::kSlots + wi) * slot_stride +
+                                                  4 * half);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const uint32_t v = w[r][wi] >> (8 * half);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            d[r][m] = dot2(xp[m].x, v & 0x00030003u, d[r][m]);
+            d[r][m] = dot2(xp[m].y, (v >> 2) & 0x00030003u, d[r][m]);
+            d[r][m] = dot2(xp[m].z, (v >> 4) & 0x00030003u, d[r][m]);
+            d[r][m] = dot2(xp[m].w, (v >> 6) & 0x00030003u, d[r][m]);
+          }
+        }
+        if constexpr (M > 2) sched_fence();
       }
     }
 #pragma unroll
@@ -138,7 +181,6 @@ __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUn
 #pragma unroll
       for (int m = 0; m < M; ++m) d[r][m] *= kDenormScale;
   } else {
-    // 2-bit: pair i of a word = codes (i, i+8), field (w >> 2i) & 0x00030003.
     // 3-bit: pair p = codes (2p, 2p+1), a 6-bit field at bit 6p of the unit.
 #pragma unroll
     for (int r = 0; r < RW; ++r)
@@ -148,23 +190,19 @@ __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUn
     for (int p = 0; p < G::kUnitPairs; ++p) {
       uint32_t xp[M];
 #pragma unroll
-      for (int m = 0; m < M; ++m) xp[m] = xu[m * m_stride + p];
+      for (int m = 0; m < M; ++m) xp[m] = xu[(m * G::kSlots + p) * slot_stride];
 #pragma unroll
       for (int r = 0; r < RW; ++r) {
-        uint32_t q;
-        if constexpr (BITS == 2) {
-          q = (w[r][p / 8] >> (2 * (p % 8))) & 0x00030003u;
-        } else {
-          const int bit = 6 * p;
-          const int word = bit >> 5;
-          const int sh = bit & 31;
-          const uint32_t f = (sh <= 26) ? (w[r][word] >> sh)
-                                        : __builtin_amdgcn_alignbit(w[r][word + 1], w[r][word], sh);
-          q = (f & 7u) | ((f << 13) & 0x70000u);
-        }
+        const int bit = 6 * p;
+        const int word = bit >> 5;
+        const int sh = bit & 31;
+        const uint32_t f = (sh <= 26) ? (w[r][word] >> sh)
+                                      : __builtin_amdgcn_alignbit(w[r][word + 1], w[r][word], sh);
+        const uint32_t q = (f & 7u) | ((f << 13) & 0x70000u);
 #pragma unroll
         for (int m = 0; m < M; ++m) d[r][m] = dot2(xp[m], q, d[r][m]);
       }
+      if constexpr (M > 4) sched_fence();
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r)
@@ -173,47 +211,213 @@ __device__ __forceinline__ void unit_dot(const uint32_t (&w)[RW][Geom<BITS>::kUn
   }
 }
 
-// Stage x[m][code0 : code0 + n_units * kUnitCodes] for all m into LDS in the
-// pair order above, and the fp32 activation sum of every unit.
+// Stage x[m][code0 : code0 + n_units * kUnitCodes] for all m into LDS
+// (slot-major, pairs in weight-word order) plus the fp32 sum of every unit.
 template <int BITS, int M>
 __device__ __forceinline__ void stage_x(const f16* __restrict__ x, int d_in, int code0,
                                         int n_units, uint32_t* xs, float* xsum) {
   using G = Geom<BITS>;
-  const int pairs_per_m = n_units * G::kUnitPairs;
+  const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);  // fp16 pairs, row m at m*d_in/2
   if constexpr (G::kMagic) {
-    // One "word block" = the kCodesPerWord codes of one weight word.
+    // Thread = one weight word's block of C codes; the four blocks of a unit
+    // are four consecutive lanes, which also sum the unit's activations.
     constexpr int C = G::kCodesPerWord;
     constexpr int H = G::kPairsPerWord;
-    const int blocks_per_m = n_units * G::kUnitWords;
-    for (int idx = threadIdx.x; idx < M * blocks_per_m; idx += kBlock) {
-      const int m = idx / blocks_per_m;
-      const int blk = idx - m * blocks_per_m;
-      const uint16_t* src =
-          reinterpret_cast<const uint16_t*>(x) + (size_t)m * d_in + code0 + blk * C;
-      uint32_t* dst = xs + m * pairs_per_m + blk * H;
+    const int total = M * n_units * 4;
+    for (int idx = threadIdx.x; idx < total; idx += kBlock) {
+      const int wi = idx & 3;
+      const int mu = idx >> 2;
+      const int m = mu / n_units;
+      const int u = mu - m * n_units;
+      const uint32_t* src = xw + ((size_t)m * d_in + code0 + (u * 4 + wi) * C) / 2;
+      uint32_t hw[C / 2];  // C halves as C/2 words
+      if constexpr (C == 8) {
+        u32x4 v = *reinterpret_cast<const u32x4*>(src);
+        hw[0] = v.x; hw[1] = v.y; hw[2] = v.z; hw[3] = v.w;
+      } else if constexpr (C == 4) {
+        u32x2 v = *reinterpret_cast<const u32x2*>(src);
+        hw[0] = v.x; hw[1] = v.y;
+      } else {
+        u32x4 v0 = *reinterpret_cast<const u32x4*>(src);
+        u32x4 v1 = *reinterpret_cast<const u32x4*>(src + 4);
+        hw[0] = v0.x; hw[1] = v0.y; hw[2] = v0.z; hw[3] = v0.w;
+        hw[4] = v1.x; hw[5] = v1.y; hw[6] = v1.z; hw[7] = v1.w;
+      }
+      uint32_t* dst = xs + ((m * G::kSlots + wi) * n_units + u) * H;
+      float part = 0.0f;
 #pragma unroll
-      for (int i = 0; i < H; ++i) dst[i] = (uint32_t)src[i] | ((uint32_t)src[i + H] << 16);
+      for (int i = 0; i < H; ++i) {
+        const uint32_t lo = (hw[i / 2] >> (16 * (i & 1))) & 0xFFFFu;
+        const uint32_t hi = (hw[(i + H) / 2] >> (16 * ((i + H) & 1))) & 0xFFFFu;
+        const uint32_t pair = lo | (hi << 16);
+        dst[i] = pair;
+        part = dot2(pair, 0x3C003C00u, part);
+      }
+      part += __shfl_xor(part, 1, 4);
+      part += __shfl_xor(part, 2, 4);
+      if (wi == 0) xsum[m * n_units + u] = part;
     }
   } else {
-    const int words_per_m = pairs_per_m;
-    for (int idx = threadIdx.x; idx < M * words_per_m; idx += kBlock) {
-      const int m = idx / words_per_m;
-      const int wi = idx - m * words_per_m;
-      const uint32_t* src = reinterpret_cast<const uint32_t*>(x + (size_t)m * d_in + code0);
-      xs[m * pairs_per_m + wi] = src[wi];
+    // 3-bit: slot p of a unit = natural activation word p; eight threads per
+    // unit each move four words.
+    const int total = M * n_units * 8;
+    for (int idx = threadIdx.x; idx < total; idx += kBlock) {
+      const int part_id = idx & 7;
+      const int mu = idx >> 3;
+      const int m = mu / n_units;
+      const int u = mu - m * n_units;
+      const uint32_t* src = xw + ((size_t)m * d_in + code0 + u * 64) / 2 + part_id * 4;
+      u32x4 v = *reinterpret_cast<const u32x4*>(src);
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+      float part = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xs[(m * G::kSlots + part_id * 4 + i) * n_units + u] = vw[i];
+        part = dot2(vw[i], 0x3C003C00u, part);
+      }
+      part += __shfl_xor(part, 1, 8);
+      part += __shfl_xor(part, 2, 8);
+      part += __shfl_xor(part, 4, 8);
+      if (part_id == 0) xsum[m * n_units + u] = part;
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < M * n_units; idx += kBlock) {
-    const int m = idx / n_units;
-    const int u = idx - m * n_units;
-    const uint32_t* p = xs + m * pairs_per_m + u * G::kUnitPairs;
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < G::kUnitPairs; ++i) s = dot2(p[i], 0x3C003C00u, s);
-    xsum[m * n_units + u] = s;
+}
+
+// Early staging for the resident path: every activation fragment a thread
+// stages is first loaded into registers, BEFORE the first weight loads are
+// issued. Loads complete in order, so the block can stage x and pass its
+// barrier as soon as x (an L2 hit) arrives, while the weights are still in
+// flight; each wave then computes the moment its own weights land.
+template <int BITS, int M>
+struct EarlyX {
+  using G = Geom<BITS>;
+  // A fragment: the codes of one weight word (magic widths) or four
+  // activation words (3-bit).
+  static constexpr int kFragWords = G::kMagic ? G::kCodesPerWord / 2 : 4;
+  static constexpr int kItemsPerUnit = G::kMagic ? 4 : 8;
+  static constexpr int kMaxItems = 32 / kFragWords;  // <= 32 VGPRs held per thread
+
+  static __device__ __forceinline__ bool fits(int units) {
+    return M * units * kItemsPerUnit <= kMaxItems * kBlock;
   }
-  __syncthreads();
+
+  // Straight-line loads (clamped indices, no branches) through a pointer
+  // without restrict, so the fence that follows keeps them ahead of the
+  // weight loads instead of letting them sink into commit().
+  static __device__ __forceinline__ void fetch(const f16* x, int d_in, int units,
+                                               uint32_t (&f)[kMaxItems][kFragWords]) {
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+    const int total = M * units * kItemsPerUnit;
+    const int n_items = (total + kBlock - 1) / kBlock;  // block-uniform
+#pragma unroll
+    for (int i = 0; i < kMaxItems; ++i) {
+      const int idx = min((int)threadIdx.x + i * kBlock, total - 1);
+      if (i < n_items) {
+        const int part = idx % kItemsPerUnit;
+        const int mu = idx / kItemsPerUnit;
+        const int m = mu / units;
+        const int u = mu - m * units;
+        const uint32_t* src;
+        if constexpr (G::kMagic)
+          src = xw + ((size_t)m * d_in + (u * 4 + part) * G::kCodesPerWord) / 2;
+        else
+          src = xw + ((size_t)m * d_in + u * 64) / 2 + part * 4;
+        if constexpr (kFragWords == 2) {
+          u32x2 v = *reinterpret_cast<const u32x2*>(src);
+          f[i][0] = v.x; f[i][1] = v.y;
+        } else {
+#pragma unroll
+          for (int j = 0; j < kFragWords; j += 4) {
+            u32x4 v = *reinterpret_cast<const u32x4*>(src + j);
+            f[i][j] = v.x; f[i][j + 1] = v.y; f[i][j + 2] = v.z; f[i][j + 3] = v.w;
+          }
+        }
+      }
+    }
+  }
+
+  static __device__ __forceinline__ void commit(const uint32_t (&f)[kMaxItems][kFragWords],
+                                                int units, uint32_t* xs, float* xsum) {
+    const int total = M * units * kItemsPerUnit;
+#pragma unroll
+    for (int i = 0; i < kMaxItems; ++i) {
+      const int idx = threadIdx.x + i * kBlock;
+      if (idx < total) {  // whole quads / octets are active together
+        const int part = idx % kItemsPerUnit;
+        const int mu = idx / kItemsPerUnit;
+        const int m = mu / units;
+        const int u = mu - m * units;
+        float sum = 0.0f;
+        if constexpr (G::kMagic) {
+          constexpr int H = G::kPairsPerWord;
+          uint32_t* dst = xs + ((m * G::kSlots + part) * units + u) * H;
+#pragma unroll
+          for (int k = 0; k < H; ++k) {
+            const uint32_t lo = (f[i][k / 2] >> (16 * (k & 1))) & 0xFFFFu;
+            const uint32_t hi = (f[i][(k + H) / 2] >> (16 * ((k + H) & 1))) & 0xFFFFu;
+            const uint32_t pair = lo | (hi << 16);
+            dst[k] = pair;
+            sum = dot2(pair, 0x3C003C00u, sum);
+          }
+          sum += __shfl_xor(sum, 1, 4);
+          sum += __shfl_xor(sum, 2, 4);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            xs[(m * G::kSlots + part * 4 + k) * units + u] = f[i][k];
+            sum = dot2(f[i][k], 0x3C003C00u, sum);
+          }
+          sum += __shfl_xor(sum, 1, 8);
+          sum += __shfl_xor(sum, 2, 8);
+          sum += __shfl_xor(sum, 4, 8);
+        }
+        if (part == 0) xsum[m * units + u] = sum;
+      }
+    }
+    __syncthreads();
+  }
+};
+
+// One pipeline step's registers: kUPL units of RW rows, with their scales.
+template <int BITS, int RW>
+struct StepRegs {
+  uint32_t w[kUPL][RW][Geom<BITS>::kUnitWords];
+  f16x2 sb[kUPL][RW];  // fp16 scale (.x) and bias (.y), loaded straight into halves
+  uint32_t valid;      // bit k: unit k of this step lies inside the row
+};
+
+
+
+// Position of a wave in its sequence of steps: chunk start c0 (units), chunk
+// size cu, step index within the chunk.
+struct StepPos {
+  int c0, cu, step, steps;
+};
+
+template <int BITS, int RW>
+__device__ __forceinline__ void load_step(StepRegs<BITS, RW>& R, const StepPos& p,
+                                          const uint32_t* __restrict__ wq,
+                                          const uint16_t* __restrict__ scales,
+                                          const uint16_t* __restrict__ biases,
+                                          const int (&rows)[RW], int row_words, int groups,
+                                          int lane, int kp, int kw) {
+  using G = Geom<BITS>;
+  constexpr int kUnitsPerGroup = 64 / G::kUnitCodes;
+  R.valid = 0;
+#pragma unroll
+  for (int k = 0; k < kUPL; ++k) {
+    const int ul = ((p.step * kUPL + k) * kw + kp) * kWave + lane;
+    R.valid |= (ul < p.cu ? 1u : 0u) << k;
+    const int u = p.c0 + min(ul, p.cu - 1);  // clamped: masked through R.valid at use
+    const int g = u / kUnitsPerGroup;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      load_unit<BITS>(wq + (size_t)rows[r] * row_words + (size_t)u * G::kUnitWords, R.w[k][r]);
+      R.sb[k][r] = f16x2{__builtin_bit_cast(f16, scales[(size_t)rows[r] * groups + g]),
+                         __builtin_bit_cast(f16, biases[(size_t)rows[r] * groups + g])};
+    }
+  }
 }
 
 template <int BITS, int M, int RW, typename OutT>
@@ -222,19 +426,23 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(const f16* __restrict__ x,
                                                      const uint16_t* __restrict__ scales,
                                                      const uint16_t* __restrict__ biases,
                                                      OutT* __restrict__ out, int d_in, int d_out,
-                                                     int chunk_units) {
+                                                     int chunk_units, int kw) {
   using G = Geom<BITS>;
-  extern __shared__ uint32_t smem[];
+  extern __shared__ __align__(16) uint32_t smem[];
   uint32_t* xs = smem;
   float* xsum = reinterpret_cast<float*>(smem + M * chunk_units * G::kUnitPairs);
+  __shared__ float red[kWavesPerBlock][RW * M];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int row0 = (blockIdx.x * kWavesPerBlock + wave) * RW;
+  const int sets = kWavesPerBlock / kw;  // row sets per block
+  const int rs = wave / kw;              // this wave's row set
+  const int kp = wave - rs * kw;         // this wave's share of every chunk
+  const int row0 = (blockIdx.x * sets + rs) * RW;
   const int units = d_in / G::kUnitCodes;
   const int row_words = units * G::kUnitWords;
   const int groups = d_in / 64;
-  constexpr int kUnitsPerGroup = 64 / G::kUnitCodes;  // 4, 2, 1 (3-bit: 1)
+  const int per_step = kUPL * kw * kWave;  // units of a chunk one step covers
 
   int rows[RW];
 #pragma unroll
@@ -246,66 +454,474 @@ __global__ __launch_bounds__(kBlock) void qmv_kernel(const f16* __restrict__ x,
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
-  for (int c0 = 0; c0 < units; c0 += chunk_units) {
-    const int cu = min(chunk_units, units - c0);
-    if (c0 > 0) __syncthreads();  // everyone is done with the previous chunk
-    stage_x<BITS, M>(x, d_in, c0 * G::kUnitCodes, cu, xs, xsum);
+  StepPos pos;
+  pos.c0 = 0;
+  pos.cu = min(chunk_units, units);
+  pos.step = 0;
+  pos.steps = (pos.cu + per_step - 1) / per_step;
+  StepRegs<BITS, RW> cur, nxt;
+  // The first step's weights are requested before the activations are
+  // staged, so HBM latency overlaps the staging.
+  load_step<BITS, RW>(cur, pos, wq, scales, biases, rows, row_words, groups, lane, kp, kw);
+  int staged = -1;
+  while (true) {
+    if (pos.c0 != staged) {  // block-uniform: every wave walks the same steps
+      if (staged >= 0) __syncthreads();
+      stage_x<BITS, M>(x, d_in, pos.c0 * G::kUnitCodes, pos.cu, xs, xsum);
+      staged = pos.c0;
+    }
+    StepPos np = pos;
+    if (++np.step == np.steps) {
+      np.c0 += chunk_units;
+      np.cu = min(chunk_units, units - np.c0);
+      np.step = 0;
+      np.steps = (np.cu + per_step - 1) / per_step;
+    }
+    const bool more = np.c0 < units;
+    if (more) load_step<BITS, RW>(nxt, np, wq, scales, biases, rows, row_words, groups, lane, kp, kw);
 
-    for (int ul = lane; ul < cu; ul += kWave) {
-      const int u = c0 + ul;
-      const int g = u / kUnitsPerGroup;
-      uint32_t w[RW][G::kUnitWords];
-      float s[RW], b[RW];
 #pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        load_unit<BITS>(wq + (size_t)rows[r] * row_words + u * G::kUnitWords, w[r]);
-      }
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        s[r] = f16_bits_to_f32(scales[(size_t)rows[r] * groups + g]);
-        b[r] = f16_bits_to_f32(biases[(size_t)rows[r] * groups + g]);
-      }
+    for (int k = 0; k < kUPL; ++k) {
+      const int ul = min(((pos.step * kUPL + k) * kw + kp) * kWave + lane, pos.cu - 1);
+      const bool valid = (cur.valid >> k) & 1u;  // a clamped unit adds exactly nothing
       float d[RW][M];
-      unit_dot<BITS, M, RW>(w, xs + ul * G::kUnitPairs, cu * G::kUnitPairs, d);
+      unit_dot<BITS, M, RW>(cur.w[k], xs + ul * G::kSlotPairs, pos.cu * G::kSlotPairs, d);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float xs_u = xsum[m * cu + ul];
+        const float xs_u = xsum[m * pos.cu + ul];
 #pragma unroll
-        for (int r = 0; r < RW; ++r) acc[r][m] = fmaf(s[r], d[r][m], fmaf(b[r], xs_u, acc[r][m]));
+        for (int r = 0; r < RW; ++r)
+        {
+          const float sc = valid ? (float)cur.sb[k][r].x : 0.0f;
+          const float bi = valid ? (float)cur.sb[k][r].y : 0.0f;
+          acc[r][m] = fmaf(sc, d[r][m], fmaf(bi, xs_u, acc[r][m]));
+        }
       }
+      if constexpr (M > 2) sched_fence();
     }
+    if (!more) break;
+    cur = nxt;
+    pos = np;
   }
 
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
+  for (int r = 0; r < RW; ++r)
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float v = wave_sum(acc[r][m]);
-      if (lane == 0 && row0 + r < d_out) store_out<OutT>(out + (size_t)m * d_out + row0 + r, v);
+    for (int m = 0; m < M; ++m) acc[r][m] = wave_sum(acc[r][m]);
+
+  if (kw == 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+          if (row0 + r < d_out) store_out<OutT>(out + (size_t)m * d_out + row0 + r, acc[r][m]);
+    }
+  } else {
+    // Waves sharing a row set hold partial sums over disjoint units; add
+    // them in wave order (deterministic) through LDS.
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) red[wave][r * M + m] = acc[r][m];
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < sets * RW * M; t += kBlock) {
+      const int set = t / (RW * M);
+      const int rm = t - set * RW * M;
+      const int r = rm / M, m = rm - r * M;
+      float v = 0.0f;
+      for (int j = 0; j < kw; ++j) v += red[set * kw + j][rm];
+      const int row = (blockIdx.x * sets + set) * RW + r;
+      if (row < d_out) store_out<OutT>(out + (size_t)m * d_out + row, v);
     }
   }
 }
 
-template <int BITS, int M, typename OutT>
+// ---------------------------------------------------------------------------
+// Resident-x path: the whole activation block (M x d_in) is staged once per
+// block and every block stays resident, looping over row sets. Each wave
+// walks its own sequence of (row set, unit step) pairs with two register
+// sets in ping-pong: the loads of step t+1 are in flight while step t
+// computes, so HBM streaming and VALU work overlap for the whole kernel
+// instead of meeting in one load-then-compute phase.
+// ---------------------------------------------------------------------------
+template <int BITS, int RW>
+__device__ __forceinline__ void load_set_step(StepRegs<BITS, RW>& R, int set, int step,
+                                              const uint32_t* __restrict__ wq,
+                                              const uint16_t* __restrict__ scales,
+                                              const uint16_t* __restrict__ biases, int d_out,
+                                              int units, int row_words, int groups, int lane) {
+  // Branch-free: a unit past the row end loads a clamped (valid) address and
+  // is masked at use through R.valid, so no load waits inside a branch.
+  using G = Geom<BITS>;
+  constexpr int kUnitsPerGroup = 64 / G::kUnitCodes;
+  R.valid = 0;
+#pragma unroll
+  for (int k = 0; k < kUPL; ++k) {
+    const int ul = (step * kUPL + k) * kWave + lane;
+    R.valid |= (ul < units ? 1u : 0u) << k;
+    const int u = min(ul, units - 1);
+    const int g = u / kUnitsPerGroup;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int row = min(set * RW + r, d_out - 1);
+      load_unit<BITS>(wq + (size_t)row * row_words + (size_t)u * G::kUnitWords, R.w[k][r]);
+      R.sb[k][r] = f16x2{__builtin_bit_cast(f16, scales[(size_t)row * groups + g]),
+                         __builtin_bit_cast(f16, biases[(size_t)row * groups + g])};
+    }
+  }
+}
+
+template <int BITS, int M, int RW>
+__device__ __forceinline__ void compute_step(const StepRegs<BITS, RW>& R, int step, int units,
+                                             const uint32_t* xs, const float* xsum, int lane,
+                                             float (&acc)[RW][M]) {
+  using G = Geom<BITS>;
+#pragma unroll
+  for (int k = 0; k < kUPL; ++k) {
+    const int ul = min((step * kUPL + k) * kWave + lane, units - 1);
+    const bool valid = (R.valid >> k) & 1u;  // a clamped unit adds exactly nothing
+    float d[RW][M];
+    unit_dot<BITS, M, RW>(R.w[k], xs + ul * G::kSlotPairs, units * G::kSlotPairs, d);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float xs_u = xsum[m * units + ul];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const float sc = valid ? (float)R.sb[k][r].x : 0.0f;
+        const float bi = valid ? (float)R.sb[k][r].y : 0.0f;
+        acc[r][m] = fmaf(sc, d[r][m], fmaf(bi, xs_u, acc[r][m]));
+      }
+    }
+    if constexpr (M > 2) sched_fence();
+  }
+}
+
+template <int RW, int M, typename OutT>
+__device__ __forceinline__ void finish_set(float (&acc)[RW][M], int set, int d_out, int lane,
+                                           OutT* __restrict__ out) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float v = wave_sum(acc[r][m]);
+      acc[r][m] = 0.0f;
+      if (lane == 0 && set * RW + r < d_out)
+        store_out<OutT>(out + (size_t)m * d_out + set * RW + r, v);
+    }
+}
+
+template <int BITS, int M, int RW, typename OutT>
+__global__ __launch_bounds__(kBlock) void qmv_resident_kernel(
+    const f16* __restrict__ x, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    OutT* __restrict__ out, int d_in, int d_out) {
+  using G = Geom<BITS>;
+  extern __shared__ __align__(16) uint32_t smem[];
+  const int units = d_in / G::kUnitCodes;
+  uint32_t* xs = smem;
+  float* xsum = reinterpret_cast<float*>(smem + M * units * G::kUnitPairs);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const int n_waves = gridDim.x * kWavesPerBlock;
+  const int row_words = units * G::kUnitWords;
+  const int groups = d_in / 64;
+  const int sets = (d_out + RW - 1) / RW;
+  const int steps_per_set = (units + kUPL * kWave - 1) / (kUPL * kWave);
+  const int my_sets = wave < sets ? (sets - 1 - wave) / n_waves + 1 : 0;
+  const int total = my_sets * steps_per_set;
+
+  StepRegs<BITS, RW> A, B;
+  using EX = EarlyX<BITS, M>;
+  if (EX::fits(units)) {  // block-uniform
+    uint32_t frag[EX::kMaxItems][EX::kFragWords];
+    EX::fetch(x, d_in, units, frag);
+    sched_fence();  // x requests go out before the weight requests
+    // Unconditional (a wave without work loads a valid row and ignores it):
+    // a branch here would make the compiler drain the x loads first.
+    load_set_step<BITS, RW>(A, min(wave, sets - 1), 0, wq, scales, biases, d_out, units,
+                            row_words, groups, lane);
+    EX::commit(frag, units, xs, xsum);  // ends with a block barrier
+  } else {
+    if (total > 0)
+      load_set_step<BITS, RW>(A, wave, 0, wq, scales, biases, d_out, units, row_words, groups,
+                              lane);
+    stage_x<BITS, M>(x, d_in, 0, units, xs, xsum);  // ends with a block barrier
+  }
+
+  float acc[RW][M];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+
+  // Step t of this wave: set wave + (t / steps_per_set) * n_waves, unit step
+  // t % steps_per_set.
+  int set = wave, step = 0;
+  for (int t = 0; t < total; t += 2) {
+    int set1 = set, step1 = step + 1;
+    if (step1 == steps_per_set) { step1 = 0; set1 += n_waves; }
+    if (t + 1 < total)
+      load_set_step<BITS, RW>(B, set1, step1, wq, scales, biases, d_out, units, row_words,
+                              groups, lane);
+    compute_step<BITS, M, RW>(A, step, units, xs, xsum, lane, acc);
+    if (step == steps_per_set - 1) finish_set<RW, M, OutT>(acc, set, d_out, lane, out);
+    if (t + 1 >= total) break;
+
+    int set2 = set1, step2 = step1 + 1;
+    if (step2 == steps_per_set) { step2 = 0; set2 += n_waves; }
+    if (t + 2 < total)
+      load_set_step<BITS, RW>(A, set2, step2, wq, scales, biases, d_out, units, row_words,
+                              groups, lane);
+    compute_step<BITS, M, RW>(B, step1, units, xs, xsum, lane, acc);
+    if (step1 == steps_per_set - 1) finish_set<RW, M, OutT>(acc, set1, d_out, lane, out);
+    set = set2;
+    step = step2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming path (small M): no LDS and no barrier. Every wave loads the
+// activation fragments of its own units (L1/L2-resident: all waves read the
+// same x) together with its weights, builds the pair order in registers with
+// byte permutes, and computes the moment its own loads land. Waves are
+// independent, so the hardware overlaps one wave's math with the next
+// wave's loads without any block-level synchronisation.
+// ---------------------------------------------------------------------------
+template <int BITS, int M, int RW>
+struct StreamRegs {
+  static constexpr int kXWords = Geom<BITS>::kUnitCodes / 2;  // natural fp16 pairs of a unit
+  uint32_t w[RW][Geom<BITS>::kUnitWords];
+  f16x2 sb[RW];
+  uint32_t x[M][kXWords];
+  bool valid;
+};
+
+template <int BITS, int M, int RW>
+__device__ __forceinline__ void stream_load(StreamRegs<BITS, M, RW>& R, int set, int ul,
+                                            const f16* __restrict__ x,
+                                            const uint32_t* __restrict__ wq,
+                                            const uint16_t* __restrict__ scales,
+                                            const uint16_t* __restrict__ biases, int d_in,
+                                            int d_out, int units, int row_words, int groups) {
+  using G = Geom<BITS>;
+  constexpr int kUnitsPerGroup = 64 / G::kUnitCodes;
+  constexpr int kXW = StreamRegs<BITS, M, RW>::kXWords;
+  R.valid = ul < units;
+  const int u = min(ul, units - 1);
+  const int g = u / kUnitsPerGroup;
+  const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < kXW; j += 4) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(xw + ((size_t)m * d_in + u * G::kUnitCodes) / 2 + j);
+      R.x[m][j] = v.x; R.x[m][j + 1] = v.y; R.x[m][j + 2] = v.z; R.x[m][j + 3] = v.w;
+    }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int row = min(set * RW + r, d_out - 1);
+    load_unit<BITS>(wq + (size_t)row * row_words + (size_t)u * G::kUnitWords, R.w[r]);
+    R.sb[r] = f16x2{__builtin_bit_cast(f16, scales[(size_t)row * groups + g]),
+                    __builtin_bit_cast(f16, biases[(size_t)row * groups + g])};
+  }
+}
+
+// Natural pairs (x0,x1),(x2,x3),... of one weight word's codes -> the pair
+// order of unit_dot: (x_i, x_{i+c/2}).
+template <int BITS>
+__device__ __forceinline__ void pair_order(const uint32_t* nat, uint32_t* out) {
+  constexpr int H = Geom<BITS>::kPairsPerWord;  // pairs per word
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    // low half of pair i = half i, high half = half i + H
+    const uint32_t a = nat[i / 2], b = nat[(i + H) / 2];
+    const uint32_t lo = (i & 1) ? (a >> 16) : (a & 0xFFFFu);
+    const uint32_t hi = ((i + H) & 1) ? (b & 0xFFFF0000u) : (b << 16);
+    out[i] = lo | hi;
+  }
+}
+
+template <int BITS, int M, int RW>
+__device__ __forceinline__ void stream_compute(const StreamRegs<BITS, M, RW>& R,
+                                               float (&acc)[RW][M]) {
+  using G = Geom<BITS>;
+  constexpr int kXW = StreamRegs<BITS, M, RW>::kXWords;
+  // Pair-ordered activations of this unit, slot-major like the LDS layout,
+  // with slot stride kSlotPairs so unit_dot reads them unchanged.
+  uint32_t xp[M * kXW];
+  float xs_u[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kXW; ++j) sum = dot2(R.x[m][j], 0x3C003C00u, sum);
+    xs_u[m] = sum;
+    if constexpr (G::kMagic) {
+      constexpr int H = G::kPairsPerWord;
+#pragma unroll
+      for (int wi = 0; wi < G::kUnitWords; ++wi)
+        pair_order<BITS>(&R.x[m][wi * (G::kCodesPerWord / 2)], &xp[(m * G::kSlots + wi) * H]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kXW; ++j) xp[m * kXW + j] = R.x[m][j];
+    }
+  }
+  float d[RW][M];
+  unit_dot<BITS, M, RW>(R.w, xp, G::kSlotPairs, d);
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const float sc = R.valid ? (float)R.sb[r].x : 0.0f;
+      const float bi = R.valid ? (float)R.sb[r].y : 0.0f;
+      acc[r][m] = fmaf(sc, d[r][m], fmaf(bi, xs_u[m], acc[r][m]));
+    }
+}
+
+template <int BITS, int M, int RW, typename OutT>
+__global__ __launch_bounds__(kBlock) void qmv_stream_kernel(
+    const f16* __restrict__ x, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    OutT* __restrict__ out, int d_in, int d_out) {
+  using G = Geom<BITS>;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int set = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const int units = d_in / G::kUnitCodes;
+  const int row_words = units * G::kUnitWords;
+  const int groups = d_in / 64;
+  const int steps = (units + kWave - 1) / kWave;
+  const int sets = (d_out + RW - 1) / RW;
+  if (set >= sets) return;  // whole waves; no barrier in this kernel
+
+  float acc[RW][M];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+
+  StreamRegs<BITS, M, RW> A, B;
+  stream_load<BITS, M, RW>(A, set, lane, x, wq, scales, biases, d_in, d_out, units, row_words,
+                           groups);
+  for (int t = 0; t < steps; t += 2) {
+    if (t + 1 < steps)
+      stream_load<BITS, M, RW>(B, set, (t + 1) * kWave + lane, x, wq, scales, biases, d_in,
+                               d_out, units, row_words, groups);
+    stream_compute<BITS, M, RW>(A, acc);
+    if (t + 1 >= steps) break;
+    if (t + 2 < steps)
+      stream_load<BITS, M, RW>(A, set, (t + 2) * kWave + lane, x, wq, scales, biases, d_in,
+                               d_out, units, row_words, groups);
+    stream_compute<BITS, M, RW>(B, acc);
+  }
+  finish_set<RW, M, OutT>(acc, set, d_out, lane, out);
+}
+
+// Largest LDS footprint the resident path accepts: at least two blocks per CU.
+constexpr size_t kResidentLdsMax = 64 * 1024;
+
+template <int BITS, int M>
+size_t resident_lds_bytes(int d_in) {
+  using G = Geom<BITS>;
+  const size_t units = d_in / G::kUnitCodes;
+  return units * (size_t)(M * G::kUnitPairs + M) * 4;
+}
+
+int env_int(const char* name, int fallback) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : fallback;
+}
+
+template <int BITS, int M, int RW, typename OutT>
 int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void* biases,
                void* out, int d_out, int d_in, hipStream_t stream) {
   using G = Geom<BITS>;
-  constexpr int RW = (M <= 2) ? 4 : (M <= 8 ? 2 : 1);
   const int units = d_in / G::kUnitCodes;
+  const size_t res_lds = resident_lds_bytes<BITS, M>(d_in);
+  // Path: 1 streaming (no LDS; M <= 2), 2 resident x, 3 chunked x. Auto
+  // (measured on MI355X): streaming for M = 1, resident when x fits, else
+  // chunked. KVP_QMV_PATH overrides for tiling sweeps.
+  int path = env_int("KVP_QMV_PATH", 0);
+  if (path == 0) path = (M == 1) ? 1 : (res_lds <= kResidentLdsMax ? 2 : 3);
+  if constexpr (M <= 2) {
+    if (path == 1) {
+      const int sets = (d_out + RW - 1) / RW;
+      const int blocks = (sets + kWavesPerBlock - 1) / kWavesPerBlock;
+      hipLaunchKernelGGL((qmv_stream_kernel<BITS, M, RW, OutT>), dim3(blocks), dim3(kBlock), 0,
+                         stream, static_cast<const f16*>(x), wq,
+                         static_cast<const uint16_t*>(scales),
+                         static_cast<const uint16_t*>(biases), static_cast<OutT*>(out), d_in,
+                         d_out);
+      return check_launch("kvp_qmv");
+    }
+  }
+  if (res_lds <= kResidentLdsMax && path != 3) {
+    // Grid = the blocks that fit on the device at once (cached per kernel
+    // and footprint), capped by the row sets there are.
+    static thread_local int cached_blocks = 0;
+    static thread_local size_t cached_lds = 0;
+    if (cached_lds != res_lds || cached_blocks == 0) {
+      int per_cu = 0, dev = 0, cus = 0;
+      hipGetDevice(&dev);
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, reinterpret_cast<const void*>(qmv_resident_kernel<BITS, M, RW, OutT>),
+              kBlock, res_lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+      cached_blocks = per_cu * cus;
+      cached_lds = res_lds;
+    }
+    const int sets = (d_out + RW - 1) / RW;
+    int blocks = min(cached_blocks, (sets + kWavesPerBlock - 1) / kWavesPerBlock);
+    blocks = env_int("KVP_QMV_BLOCKS", blocks);
+    if (blocks < 1) return set_error(KVP_INVALID, "kvp_qmv: KVP_QMV_BLOCKS=%d", blocks);
+    hipLaunchKernelGGL((qmv_resident_kernel<BITS, M, RW, OutT>), dim3(blocks), dim3(kBlock),
+                       res_lds, stream, static_cast<const f16*>(x), wq,
+                       static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases),
+                       static_cast<OutT*>(out), d_in, d_out);
+    return check_launch("kvp_qmv");
+  }
   // Chunk = whole 64-unit lane rounds that fit the staging budget (fewer
   // units only when one round does not fit).
   const int words_per_unit = M * G::kUnitPairs + M;  // pairs + one fp32 sum per m
   int chunk_units = kStageWords / words_per_unit;
   if (chunk_units >= kWave) chunk_units = chunk_units / kWave * kWave;
   if (chunk_units > units) chunk_units = units;
+  // Split each row's units over kw waves when rows alone leave the GPU
+  // short of waves (about 4 per SIMD on 256 CUs), but never so far that a
+  // wave has no full step of work.
+  const int rounds = (units + kWave - 1) / kWave;
+  const int row_waves = (d_out + RW - 1) / RW;
+  int kw = 1;
+  while (kw < kWavesPerBlock && row_waves * kw < 4096 && 2 * kw * kUPL <= rounds) kw *= 2;
+  kw = env_int("KVP_QMV_KW", kw);
+  if (kw != 1 && kw != 2 && kw != 4) return set_error(KVP_INVALID, "kvp_qmv: KVP_QMV_KW=%d", kw);
   const size_t lds = (size_t)chunk_units * words_per_unit * 4;
-  const int rows_per_block = kWavesPerBlock * RW;
+  const int rows_per_block = (kWavesPerBlock / kw) * RW;
   const int blocks = (d_out + rows_per_block - 1) / rows_per_block;
   hipLaunchKernelGGL((qmv_kernel<BITS, M, RW, OutT>), dim3(blocks), dim3(kBlock), lds, stream,
                      static_cast<const f16*>(x), wq, static_cast<const uint16_t*>(scales),
                      static_cast<const uint16_t*>(biases), static_cast<OutT*>(out), d_in, d_out,
-                     chunk_units);
+                     chunk_units, kw);
   return check_launch("kvp_qmv");
+}
+
+// Rows per wave: the VGPR budget of RW * M accumulators. M <= 2 can run
+// RW = 2 or 4 (KVP_QMV_RW picks for tiling sweeps); wider M steps down.
+template <int BITS, int M, typename OutT>
+int launch_qmv_rw(const void* x, const uint32_t* wq, const void* scales, const void* biases,
+                  void* out, int d_out, int d_in, hipStream_t stream) {
+  if constexpr (M <= 2) {
+    if (env_int("KVP_QMV_RW", 2) == 4)
+      return launch_qmv<BITS, M, 4, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
+    return launch_qmv<BITS, M, 2, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
+  } else {
+    constexpr int RW = (M <= 8) ? 2 : 1;
+    return launch_qmv<BITS, M, RW, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
+  }
 }
 
 template <int BITS, typename OutT>
@@ -313,7 +929,7 @@ int dispatch_m(int m, const void* x, const uint32_t* wq, const void* s, const vo
                int d_out, int d_in, hipStream_t st) {
   switch (m) {
 #define KVP_M(N) \
-  case N: return launch_qmv<BITS, N, OutT>(x, wq, s, b, out, d_out, d_in, st);
+  case N: return launch_qmv_rw<BITS, N, OutT>(x, wq, s, b, out, d_out, d_in, st);
     KVP_M(1) KVP_M(2) KVP_M(3) KVP_M(4) KVP_M(5) KVP_M(6) KVP_M(7) KVP_M(8)
     KVP_M(9) KVP_M(10) KVP_M(11) KVP_M(12) KVP_M(13) KVP_M(14) KVP_M(15) KVP_M(16)
 #undef KVP_M

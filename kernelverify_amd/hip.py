@@ -59,6 +59,12 @@ def runtime() -> ctypes.CDLL:
         "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp],
         "hipGetLastError": [],
         "hipMemGetInfo": [ctypes.POINTER(sz), ctypes.POINTER(sz)],
+        "hipStreamBeginCapture": [vp, i],
+        "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+        "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, sz],
+        "hipGraphLaunch": [vp, vp],
+        "hipGraphExecDestroy": [vp],
+        "hipGraphDestroy": [vp],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
@@ -218,5 +224,54 @@ class Event:
         try:
             if self.handle:
                 runtime().hipEventDestroy(ctypes.c_void_p(self.handle))
+        except Exception:
+            pass
+
+
+HIP_STREAM_CAPTURE_RELAXED = 2
+
+
+class Graph:
+    """A captured sequence of launches on one stream, replayed as one graph.
+
+    ``Graph(stream, fn)`` calls ``fn()`` while ``stream`` is in capture mode
+    (every kernel ``fn`` enqueues on that stream becomes a node), then
+    instantiates the graph. ``launch()`` replays it on the same stream. The
+    pack's calls allocate nothing and record no memset, so they capture.
+    """
+
+    def __init__(self, stream: Stream, fn):
+        self.stream = stream
+        rt = runtime()
+        check(rt.hipStreamBeginCapture(ctypes.c_void_p(stream.handle),
+                                       HIP_STREAM_CAPTURE_RELAXED), "hipStreamBeginCapture")
+        graph = ctypes.c_void_p()
+        try:
+            fn()
+        finally:
+            check(rt.hipStreamEndCapture(ctypes.c_void_p(stream.handle), ctypes.byref(graph)),
+                  "hipStreamEndCapture")
+        self.graph = graph.value
+        exe = ctypes.c_void_p()
+        check(rt.hipGraphInstantiate(ctypes.byref(exe), ctypes.c_void_p(self.graph), None, None,
+                                     0), "hipGraphInstantiate")
+        self.exec = exe.value
+
+    def launch(self) -> None:
+        check(runtime().hipGraphLaunch(ctypes.c_void_p(self.exec),
+                                       ctypes.c_void_p(self.stream.handle)), "hipGraphLaunch")
+
+    def destroy(self) -> None:
+        rt = runtime()
+        if getattr(self, "exec", None):
+            rt.hipGraphExecDestroy(ctypes.c_void_p(self.exec))
+            self.exec = None
+        if getattr(self, "graph", None):
+            rt.hipGraphDestroy(ctypes.c_void_p(self.graph))
+            self.graph = None
+
+    def __del__(self):
+        try:
+            self.destroy()
         except Exception:
             pass

@@ -7,11 +7,13 @@ layout (code stream + fp16 scale/bias per 64-code group), the same output
 the weights stream from HBM once whatever M is.
 
 What differs is the tiling, chosen for CDNA4 rather than inherited from the
-Metal register wall (wide_qmv.py:17-26): 64-lane waves own RW rows (4 for
-M <= 2, 2 for M <= 8, 1 above), lanes stream 16-byte units, activations are
-staged in LDS in the weight words' pair order, and codes multiply as exact
-fp16 denormals through V_DOT2_F32_F16. Widths 2, 3, 4 and 8 bits are all
-served (the reference kernel stops at 4, :140).
+Metal register wall (wide_qmv.py:17-26): 64-lane waves own RW rows (2 for
+M <= 8, 1 above), lanes stream 16-byte units, and codes multiply as exact
+fp16 denormals through V_DOT2_F32_F16. Three kernel paths share that core:
+streaming (M = 1: each wave loads its own activation fragments, no LDS, no
+barrier), resident (x staged once per persistent block) and chunked (x too
+large for LDS, staged in chunks). Widths 2, 3, 4 and 8 bits are all served
+(the reference kernel stops at 4, :140).
 """
 
 from __future__ import annotations
@@ -33,7 +35,7 @@ OUT_DTYPES = {"float16": lib.KVP_F16, "float32": lib.KVP_F32}
 
 def rows_per_wave(m: int) -> int:
     """RW: rows a wave walks together (the VGPR budget of M * RW accumulators)."""
-    return 4 if m <= 2 else (2 if m <= 8 else 1)
+    return 2 if m <= 8 else 1
 
 
 def launch_config(d_out: int, m: int) -> tuple:
@@ -90,6 +92,27 @@ def run_qmv(x: DeviceArray, w_q: DeviceArray, scales: DeviceArray, biases: Devic
     lib.check(lib.load().kvp_qmv(x.ptr, w_q.ptr, scales.ptr, biases.ptr, out.ptr,
                                  OUT_DTYPES[out.dtype.name], m, d_out, d_in, bits,
                                  getattr(stream, "handle", stream)))
+
+
+class QmvCall:
+    """One validated qmv launch with its ctypes arguments bound once.
+
+    For serving loops and graph capture: ``call(stream)`` is a bare C call,
+    no per-launch Python shape checks.
+    """
+
+    def __init__(self, x: DeviceArray, w_q: DeviceArray, scales: DeviceArray,
+                 biases: DeviceArray, out: DeviceArray, *, bits: int):
+        m, d_out, d_in = check_shapes(x, w_q, scales, biases, out, bits)
+        self._fn = lib.load().kvp_qmv
+        self._args = (x.ptr, w_q.ptr, scales.ptr, biases.ptr, out.ptr,
+                      OUT_DTYPES[out.dtype.name], m, d_out, d_in, bits)
+        self._keep = (x, w_q, scales, biases, out)
+
+    def __call__(self, stream=None) -> None:
+        status = self._fn(*self._args, getattr(stream, "handle", stream))
+        if status:
+            lib.check(status)
 
 
 def qmv(x: np.ndarray, w_q: np.ndarray, scales: np.ndarray, biases: np.ndarray, *, bits: int,
