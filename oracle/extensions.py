@@ -10,6 +10,11 @@ reference's own contracts in the way the reference's tests already do:
 - ``kv_per_sequence``: one B=1 oracle case per sequence with its own cache
   and length, the batch-row independence of
   ``tests/test_pack_kv_attention.py:120-130``.
+- ``kv_reference_gqa`` / ``kv_tolerance_gqa``: the same reference and the same
+  four members with query head h indexing cache head h // r instead of a
+  tiled copy (identical per-head arithmetic; long contexts no longer
+  quantize r copies of the cache). Pinned to the tiled form by
+  tests/test_oracle_kv_gqa.py.
 - ``route_topk``: the routing contract of ``schemas/native_ops.py:193-206`` at
   any k, from logits given directly (config 5 draws logits, not x @ router).
 - ``permute_by_expert``: the stable counting sort of (token, slot) pairs by
@@ -30,6 +35,7 @@ from __future__ import annotations
 import numpy as np
 
 from oracle.floor import floored_tolerance
+from oracle.native_kernels import _cache_dequant
 from oracle.native_ops import K_QUANT, _base_tol, kv_reference, kv_tolerance, route_probs
 from oracle.quant_contract import ENSEMBLE, QuantArtefact, dequantize
 from oracle.verify import _Case, kv_inputs
@@ -45,20 +51,102 @@ def kv_gqa_inputs(q, k_cache, v_cache, new_k, new_v, bits):
     return kv_inputs(q, tile(k_cache, 0), tile(v_cache, 0), tile(new_k, 1), tile(new_v, 1), bits)
 
 
+def _gqa_dequant(cache, bits):
+    """The fp64 view of a canonically quantized (HKV, T, DH) cache, exactly as
+    ``native_ops._kv_dequant64`` forms it (fp32 dequant, then widened)."""
+    return _cache_dequant(cache, bits).astype(np.float64)
+
+
+def kv_reference_gqa(q, k_cache, v_cache, new_k, new_v, bits, kd=None, vd=None):
+    """``kv_reference`` with query head h reading cache head h // r, without
+    tiling the cache: q (B, H, DH); caches (HKV, T, DH); new_k/new_v
+    (B, HKV, DH). Same fp64 formula (native_ops.kv_reference); the tiled form
+    pins it (tests/test_oracle_kv_gqa.py)."""
+    b, h, dh = q.shape
+    hkv = k_cache.shape[0]
+    r = h // hkv
+    kd = _gqa_dequant(k_cache, bits) if kd is None else kd
+    vd = _gqa_dequant(v_cache, bits) if vd is None else vd
+    q64 = q.astype(np.float64).reshape(b, hkv, r, dh)
+    scale = 1.0 / np.sqrt(float(dh))
+    scores = np.einsum("bgrd,gtd->bgrt", q64, kd) * scale
+    s_new = np.sum(q64 * new_k.astype(np.float64)[:, :, None, :], axis=-1) * scale
+    scores = np.concatenate([scores, s_new[..., None]], axis=-1)
+    probs = np.exp(scores - scores.max(axis=-1, keepdims=True))
+    probs /= probs.sum(axis=-1, keepdims=True)
+    out = np.einsum("bgrt,gtd->bgrd", probs[..., :-1], vd)
+    out = out + probs[..., -1][..., None] * new_v.astype(np.float64)[:, :, None, :]
+    return out.reshape(b, h, dh)
+
+
+def _kv_member_gqa(q, kd64, vd64, new_k, new_v, *, scores_order, combine_order):
+    """``native_ops._kv_member`` with the head mapping h -> h // r: per query
+    head, the same fp32 operations in the same order as on the tiled cache."""
+    b, h, dh = q.shape
+    hkv = kd64.shape[0]
+    r = h // hkv
+    q32 = q.astype(np.float32)
+    kd = kd64.astype(np.float32)
+    vd = vd64.astype(np.float32)
+    nk = np.repeat(new_k.astype(np.float32), r, axis=1)
+    nv = np.repeat(new_v.astype(np.float32), r, axis=1)
+    scale = np.float32(1.0 / np.sqrt(float(dh)))
+    t = kd.shape[1]
+    scores = np.empty((b, h, t), dtype=np.float32)
+    for hh in range(h):
+        g = hh // r
+        if scores_order == "serial":
+            prods = q32[:, hh, None, :] * kd[None, g]
+            scores[:, hh] = np.add.accumulate(prods, axis=-1, dtype=np.float32)[..., -1]
+        else:
+            scores[:, hh] = np.einsum("bd,td->bt", q32[:, hh], kd[g])
+    scores = scores * scale
+    s_new = np.sum(q32 * nk, axis=-1) * scale
+    scores = np.concatenate([scores, s_new[..., None]], axis=-1)
+    probs = np.exp(scores - scores.max(axis=-1, keepdims=True))
+    probs /= probs.sum(axis=-1, keepdims=True)
+    pc = probs[..., :-1]
+    out = np.empty(q.shape, dtype=np.float32)
+    for hh in range(h):
+        g = hh // r
+        if combine_order in ("serial", "reversed"):
+            contrib = pc[:, hh, :, None] * vd[None, g]
+            if combine_order == "reversed":
+                contrib = contrib[:, ::-1, :]
+            out[:, hh] = np.add.accumulate(contrib, axis=1, dtype=np.float32)[:, -1]
+        else:
+            out[:, hh] = np.einsum("bt,td->bd", pc[:, hh], vd[g])
+    out = out + probs[..., -1][..., None] * nv
+    return out.astype(q.dtype)
+
+
+def kv_tolerance_gqa(dtype, q, k_cache, v_cache, new_k, new_v, bits, ref, kd=None, vd=None):
+    """``kv_tolerance`` over the four KV members in their GQA-indexed form."""
+    from oracle.native_ops import KV_MEMBERS, K_QUANT
+
+    kd = _gqa_dequant(k_cache, bits) if kd is None else kd
+    vd = _gqa_dequant(v_cache, bits) if vd is None else vd
+    return floored_tolerance(_base_tol(dtype, ref), K_QUANT,
+                             (_kv_member_gqa(q, kd, vd, new_k, new_v, **kw)
+                              for kw in KV_MEMBERS.values()), ref)
+
+
 def kv_per_sequence(q, k_caches, v_caches, new_k, new_v, lengths, bits, dtype="float16",
                     with_tolerance=True):
-    """Reference (B, H, DH) and the worst per-sequence tolerance.
+    """Reference (B, H, DH) and the per-sequence tolerances.
 
     k_caches/v_caches: per-sequence raw caches (HKV, T_b, DH) of length
-    ``lengths[b]`` (extra rows past the length are ignored)."""
+    ``lengths[b]`` (extra rows past the length are ignored). Each sequence
+    is an independent B = 1 case in the GQA-indexed form."""
     refs, tols = [], []
     for b, t in enumerate(lengths):
-        inputs = kv_gqa_inputs(q[b:b + 1], k_caches[b][:, :t], v_caches[b][:, :t],
-                               new_k[b:b + 1], new_v[b:b + 1], bits)
-        ref = kv_reference(inputs)
+        kc, vc = k_caches[b][:, :t], v_caches[b][:, :t]
+        kd, vd = _gqa_dequant(kc, bits), _gqa_dequant(vc, bits)
+        args = (q[b:b + 1], kc, vc, new_k[b:b + 1], new_v[b:b + 1], bits)
+        ref = kv_reference_gqa(*args, kd=kd, vd=vd)
         refs.append(ref)
         if with_tolerance:
-            tols.append(kv_tolerance(_Case(dtype), inputs, ref))
+            tols.append(kv_tolerance_gqa(dtype, *args, ref, kd=kd, vd=vd))
     return np.concatenate(refs, axis=0), (tols if with_tolerance else None)
 
 

@@ -47,3 +47,21 @@ def test_argument_errors_are_statuses_not_crashes():
     assert "null pointer" in lib.last_error()
     with pytest.raises(lib.InvalidArgument):
         lib.check(rc)
+
+
+def declared_arities():
+    """name -> number of parameters, parsed from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(kvp_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_arities_match_header():
+    """Every ctypes prototype takes exactly the header's parameter count."""
+    arities = declared_arities()
+    assert set(arities) == set(lib.SIGNATURES)
+    for name, (_, args) in lib.SIGNATURES.items():
+        assert len(args) == arities[name], (name, len(args), arities[name])
