@@ -100,6 +100,81 @@ class QmvWorkload:
         return lambda: quantized_matmul_artefact(self.x, art)
 
 
+class KvWorkload:
+    """One decode step of quantized-KV attention (BASELINE configs 3/4 and
+    the 32k-context target): K, V ~ N(0, 1) fp16 quantized on the GPU
+    (``kvp_quantize_affine``), rotated over >= 1 GiB of device copies."""
+
+    def __init__(self, lengths, n_heads=32, n_kv_heads=8, head_dim=128, bits=4,
+                 per_sequence=False, t_stride=None, seed=0):
+        from kernelverify_amd import hip
+        from kernelverify_amd.hip import DeviceArray
+        from kernelverify_amd.pack import kv_attention
+        from kernelverify_amd.pack.quant import quantize_affine
+
+        self.lengths = [int(t) for t in lengths]
+        b = len(self.lengths)
+        t_stride = t_stride or max(self.lengths)
+        self.bits, self.b, self.h, self.hkv, self.dh = bits, b, n_heads, n_kv_heads, head_dim
+        self.per_sequence = per_sequence
+        c = b if per_sequence else 1
+        lens = "x".join(map(str, self.lengths)) if b <= 2 else f"{b} seqs"
+        self.name = f"kv {bits}b B{b} H{n_heads}/{n_kv_heads} DH{head_dim} T{lens}"
+        rng = np.random.default_rng(seed)
+        self.q = rng.standard_normal((b, n_heads, head_dim)).astype(np.float16)
+        self.nk = rng.standard_normal((b, n_kv_heads, head_dim)).astype(np.float16)
+        self.nv = rng.standard_normal((b, n_kv_heads, head_dim)).astype(np.float16)
+        self.k_raw = rng.standard_normal((c, n_kv_heads, t_stride, head_dim)).astype(np.float16)
+        self.v_raw = rng.standard_normal((c, n_kv_heads, t_stride, head_dim)).astype(np.float16)
+        shape = (c, n_kv_heads, t_stride, head_dim) if per_sequence else (n_kv_heads, t_stride,
+                                                                          head_dim)
+        k = quantize_affine(DeviceArray.from_host(self.k_raw.reshape(shape)), bits)
+        v = quantize_affine(DeviceArray.from_host(self.v_raw.reshape(shape)), bits)
+        hip.synchronize()
+        self.bytes = kv_attention.algorithmic_bytes(self.lengths, n_heads, n_kv_heads, head_dim,
+                                                    bits)
+        cache_bytes = sum(a.nbytes for a in (*k, *v))
+        copies = max(2, -(-ROTATION_BYTES // cache_bytes))
+        self.dq = DeviceArray.from_host(self.q)
+        self.dnk, self.dnv = DeviceArray.from_host(self.nk), DeviceArray.from_host(self.nv)
+        self.dt = DeviceArray.from_host(np.array(self.lengths, dtype=np.int32))
+        self.out = DeviceArray((b, n_heads, head_dim), np.float16)
+        self.calls = []
+        ws = None
+        for i in range(copies):
+            parts = [a if i == 0 else DeviceArray.from_host(a.to_host()) for a in (*k, *v)]
+            call = kv_attention.KvDecodeCall(self.dq, *parts[:3], *parts[3:], self.dnk, self.dnv,
+                                             self.dt, self.out, bits=bits,
+                                             cache_per_sequence=per_sequence, workspace=ws)
+            ws = call.workspace
+            self.calls.append(call)
+        self.i = 0
+
+    def step(self, stream):
+        self.calls[self.i % len(self.calls)](stream)
+        self.i += 1
+
+    def gpu_output(self):
+        from kernelverify_amd import hip
+
+        self.step(None)
+        hip.synchronize()
+        return self.out.to_host()
+
+    def check(self, got):
+        """max |gpu - fp64 reference| against 4 eps16 max|ref|, per sequence."""
+        from oracle.extensions import kv_reference_gqa
+
+        worst = 0.0
+        for i, t in enumerate(self.lengths):
+            c = i if self.per_sequence else 0
+            ref = kv_reference_gqa(self.q[i:i + 1], self.k_raw[c][:, :t], self.v_raw[c][:, :t],
+                                   self.nk[i:i + 1], self.nv[i:i + 1], self.bits)
+            err = float(np.max(np.abs(got[i:i + 1].astype(np.float64) - ref)))
+            worst = max(worst, err / (4 * 9.77e-4 * float(np.max(np.abs(ref)))))
+        return worst
+
+
 def time_steps(workload, steps: int, warmup: int, graph: bool = True):
     """ms per step over EXACTLY ``steps`` back-to-back launches.
 
@@ -217,6 +292,23 @@ def main() -> int:
             log(f"[bench] {secondary[-1]}")
             del w
 
+    kv = []
+    for kw in (dict(lengths=[32768], bits=4), dict(lengths=[8192], bits=8),
+               dict(lengths=list(np.random.default_rng(0).integers(1024, 32769, 8)), bits=4,
+                    per_sequence=True, t_stride=32768)):
+        w = KvWorkload(**kw)
+        ratio = w.check(w.gpu_output())
+        if not ratio <= 1.0:
+            log(f"[bench] verify FAILED {w.name}: error {ratio:.2f} x bound")
+            continue
+        ms2 = time_steps(w, max(200, args.steps // 2), args.warmup)
+        gbs2 = w.bytes / (ms2 * 1e-3) / 1e9
+        kv.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3), "GBps": round(gbs2, 1),
+                   "frac_8TBps": round(gbs2 / PEAK_HBM_GBS, 4), "bytes": w.bytes,
+                   "verify_err_over_bound": round(ratio, 4)})
+        log(f"[bench] {kv[-1]}")
+        del w
+
     cpu = None
     if not args.no_cpu:
         best, med, n = cpu_baseline(ref_fn)
@@ -243,6 +335,8 @@ def main() -> int:
     }
     if secondary:
         line["secondary"] = secondary
+    if kv:
+        line["kv_decode"] = kv
     print(json.dumps(line), flush=True)
     return 0
 

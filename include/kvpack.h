@@ -64,6 +64,20 @@ int kvp_device_info(int device, char* name, size_t name_cap, char* arch, size_t 
                     size_t* lds_per_block, size_t* global_mem_bytes, int* clock_khz);
 
 /* ------------------------------------------------------------------------
+ * MLX-affine group quantization of fp16 rows into the kernel layout.
+ * Replaces canonical_quantize + pack_codes
+ * (kernelverify/schemas/quant_contract.py:60-104, pack/wide_qmv.py:185-201)
+ * and quantize_cache (kernelverify/pack/kv_attention.py:270-283); bit-exact
+ * with the contract's fp32 algorithm.
+ *   w      fp16   [rows][cols], cols % 64 == 0
+ *   w_q    uint32 [rows][cols * bits / 32]
+ *   scales, biases fp16 [rows][cols / 64]
+ * bits in {2, 3, 4, 8}.
+ * ---------------------------------------------------------------------- */
+int kvp_quantize_affine(const void* w, int rows, int cols, int bits, uint32_t* w_q,
+                        void* scales, void* biases, void* stream);
+
+/* ------------------------------------------------------------------------
  * Quantized matvec: out[m, r] = sum_k x[m, k] * (scale[r, k/64] * q[r, k]
  *                                                + bias[r, k/64])
  * Replaces the runner-door kernel `kv_wide_qmv`

@@ -57,6 +57,7 @@ SIGNATURES = {
     "kvp_version": (_cp, []),
     "kvp_last_error": (_sz, [_cp, _sz]),
     "kvp_device_info": (_i, [_i, _cp, _sz, _cp, _sz, _ip, _ip, _szp, _szp, _ip]),
+    "kvp_quantize_affine": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "kvp_qmv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvp_kv_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "kvp_kv_decode": (_i, [_vp] * 11 + [_i] * 9 + [_vp, _sz, _vp]),

@@ -40,15 +40,22 @@ def should_dispatch(t: int) -> bool:
     return t >= 0
 
 
-def launch_config(batch: int, n_kv_heads: int, t_stride: int, chunk: int | None = None):
-    """(split grid, combine grid, chunk): the library's own chunk choice when None."""
+def max_chunk(bits: int) -> int:
+    """Largest chunk a block takes (its prefetched codes live in registers)."""
+    return 128
+
+
+def launch_config(batch: int, n_kv_heads: int, t_stride: int, bits: int = 4,
+                  chunk: int | None = None):
+    """(grid, block, chunk): one block per (chunk, KV head, sequence); the
+    library's own chunk choice (about 1024 blocks) when ``chunk`` is None."""
     if not chunk:
-        target = batch * n_kv_heads * t_stride // 2048
+        target = batch * n_kv_heads * t_stride // 1024
         chunk = 64
-        while chunk < 1024 and chunk < target:
+        while chunk < max_chunk(bits) and chunk < target:
             chunk *= 2
     n_chunks = max(1, -(-t_stride // chunk))
-    return (n_chunks, n_kv_heads, batch), None, chunk
+    return (n_chunks, n_kv_heads, batch), (256, 1, 1), chunk
 
 
 def cache_bytes(t: int, head_dim: int, bits: int) -> int:
@@ -116,10 +123,12 @@ class KvDecodeCall:
             raise lib.InvalidArgument("kv_decode: t_cached must be int32 (B,)")
         if out.shape != (b, h, dh) or out.dtype.name not in OUT_DTYPES:
             raise lib.InvalidArgument(f"kv_decode: out must be fp16/fp32 {(b, h, dh)}")
-        _, _, chunk = launch_config(b, hkv, t_stride, chunk or None)
+        _, _, chunk = launch_config(b, hkv, t_stride, bits, chunk or None)
         need = workspace_bytes(b, h, dh, t_stride, chunk)
         if workspace is None:
             workspace = DeviceArray((max(need, 4),), np.uint8)
+        elif workspace.nbytes < need:
+            raise lib.InvalidArgument(f"kv_decode: workspace {workspace.nbytes} < {need} bytes")
         self.workspace = workspace
         self._fn = lib.load().kvp_kv_decode
         self._args = (q.ptr, k_wq.ptr, k_s.ptr, k_b.ptr, v_wq.ptr, v_s.ptr, v_b.ptr, new_k.ptr,
