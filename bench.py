@@ -175,6 +175,84 @@ class KvWorkload:
         return worst
 
 
+class MoeWorkload:
+    """One MoE decode step of BASELINE config 5: route top-8 of 128 experts
+    from fp32 N(0, 1) logits, then the SwiGLU experts (gate/up 768 x 2048,
+    down 2048 x 768, 4-bit) for n tokens. Expert sets rotate over >= 1 GiB."""
+
+    def __init__(self, n, n_experts=128, k=8, d_model=2048, d_ffn=768, bits=4, seed=0):
+        from kernelverify_amd import hip
+        from kernelverify_amd.hip import DeviceArray
+        from kernelverify_amd.pack import moe_dispatch as moe
+        from kernelverify_amd.pack.quant import quantize_affine
+
+        self.n, self.e, self.k, self.dm, self.df, self.bits = n, n_experts, k, d_model, d_ffn, bits
+        self.name = f"moe {bits}b E{n_experts} top{k} {d_model}/{d_ffn} n{n}"
+        rng = np.random.default_rng(seed)
+        self.x = rng.standard_normal((n, d_model)).astype(np.float16)
+        self.logits = rng.standard_normal((n, n_experts)).astype(np.float32)
+        self.raw = [(rng.standard_normal(shape) * 0.02).astype(np.float16)
+                    for shape in ((n_experts, d_ffn, d_model), (n_experts, d_ffn, d_model),
+                                  (n_experts, d_model, d_ffn))]
+        mats = [quantize_affine(DeviceArray.from_host(w), bits) for w in self.raw]
+        hip.synchronize()
+        set_bytes = sum(a.nbytes for m in mats for a in m)
+        copies = max(2, -(-ROTATION_BYTES // set_bytes))
+        self.dx = DeviceArray.from_host(self.x)
+        self.dl = DeviceArray.from_host(self.logits)
+        self.idx = DeviceArray((n, k), np.uint32)
+        self.gate = DeviceArray((n, k), np.float32)
+        self.out = DeviceArray((n, d_model), np.float16)
+        self._route = moe.route_logits
+        self.calls = []
+        ws = None
+        for i in range(copies):
+            m = mats if i == 0 else [tuple(DeviceArray.from_host(a.to_host()) for a in t)
+                                     for t in mats]
+            call = moe.SwigluCall(self.dx, self.idx, self.gate, *m, self.out, bits=bits,
+                                  workspace=ws)
+            ws = call.workspace
+            self.calls.append(call)
+        moe.route_logits(self.dl, self.idx, self.gate, k)
+        hip.synchronize()
+        self.routed = self.idx.to_host()
+        self.bytes = moe.algorithmic_bytes(self.routed, n_experts, d_model, d_ffn, bits)
+        self.unique = len(np.unique(self.routed))
+        self.i = 0
+
+    def step(self, stream):
+        self._route(self.dl, self.idx, self.gate, self.k, stream)
+        self.calls[self.i % len(self.calls)](stream)
+        self.i += 1
+
+    def gpu_output(self):
+        from kernelverify_amd import hip
+
+        self.step(None)
+        hip.synchronize()
+        return self.out.to_host()
+
+    def check(self, got, tokens=(0,)):
+        """Error over 4 eps16 max|ref| on a few tokens (fp64 SwiGLU reference)."""
+        from oracle.extensions import artefact_from_arrays, route_topk, swiglu_reference
+        from oracle.quant_contract import QuantContract, canonical_quantize
+
+        idx, gate = route_topk(self.logits, self.k)
+        worst = 0.0
+        for t in tokens:
+            used = sorted(set(int(e) for e in idx[t]))
+            arts = []
+            for w in self.raw:
+                per = {}
+                for e in used:
+                    per[e] = canonical_quantize(w[e], QuantContract(bits=self.bits, group_size=64))
+                arts.append(per)
+            ref = swiglu_reference(self.x[t:t + 1], idx[t:t + 1], gate[t:t + 1], *arts)
+            err = float(np.max(np.abs(got[t:t + 1].astype(np.float64) - ref)))
+            worst = max(worst, err / (4 * 9.77e-4 * float(np.max(np.abs(ref)))))
+        return worst
+
+
 def time_steps(workload, steps: int, warmup: int, graph: bool = True):
     """ms per step over EXACTLY ``steps`` back-to-back launches.
 
@@ -222,6 +300,19 @@ def cpu_baseline(fn, budget_s: float = 12.0, min_reps: int = 3):
     return min(times), float(np.median(times)), len(times)
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "qmv_4b_14336x4096_m1.traffic.json"
+
+
+def measured_traffic():
+    """HBM bytes per headline launch from the committed rocprofv3 --pmc runs
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the same counter's
+    reading on a copy kernel of known size); None before that profile exists."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text())["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def blas_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
@@ -238,7 +329,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--secondary", action="store_true", help="also time the secondary configs")
+    ap.add_argument("--secondary", action="store_true", help="also time the secondary qmv configs")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the headline qmv workload (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
@@ -293,7 +386,7 @@ def main() -> int:
             del w
 
     kv = []
-    for kw in (dict(lengths=[32768], bits=4), dict(lengths=[8192], bits=8),
+    for kw in () if args.headline_only else (dict(lengths=[32768], bits=4), dict(lengths=[8192], bits=8),
                dict(lengths=list(np.random.default_rng(0).integers(1024, 32769, 8)), bits=4,
                     per_sequence=True, t_stride=32768)):
         w = KvWorkload(**kw)
@@ -307,6 +400,22 @@ def main() -> int:
                    "frac_8TBps": round(gbs2 / PEAK_HBM_GBS, 4), "bytes": w.bytes,
                    "verify_err_over_bound": round(ratio, 4)})
         log(f"[bench] {kv[-1]}")
+        del w
+
+    moe_rows = []
+    for n in () if args.headline_only else (1, 8, 32):
+        w = MoeWorkload(n)
+        ratio = w.check(w.gpu_output(), tokens=(0, n - 1) if n > 1 else (0,))
+        if not ratio <= 1.0:
+            log(f"[bench] verify FAILED {w.name}: error {ratio:.2f} x bound")
+            continue
+        ms3 = time_steps(w, max(200, args.steps // 4), args.warmup)
+        gbs3 = w.bytes / (ms3 * 1e-3) / 1e9
+        moe_rows.append({"workload": w.name, "us_per_call": round(ms3 * 1e3, 3),
+                         "GBps": round(gbs3, 1), "frac_8TBps": round(gbs3 / PEAK_HBM_GBS, 4),
+                         "unique_experts": w.unique, "bytes": w.bytes,
+                         "verify_err_over_bound": round(ratio, 4)})
+        log(f"[bench] {moe_rows[-1]}")
         del w
 
     cpu = None
@@ -330,13 +439,16 @@ def main() -> int:
         "config": {"workload": head.name, "d_out": 14336, "d_in": 4096, "bits": 4, "group": 64,
                    "batch": 1, "rotation_copies": len(head.copies)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic()},
         "cpu_baseline": cpu,
     }
     if secondary:
         line["secondary"] = secondary
     if kv:
         line["kv_decode"] = kv
+    if moe_rows:
+        line["moe"] = moe_rows
     print(json.dumps(line), flush=True)
     return 0
 

@@ -105,5 +105,17 @@ def measure(shapes=(33_067_008, 37_769_216, 9_453_568)) -> dict:
 
 if __name__ == "__main__":
     import json
+    import sys
 
-    print(json.dumps(measure(), indent=1))
+    if "--copy-only" in sys.argv:
+        # One 256 MiB copy: the calibration kernel for FETCH_SIZE/WRITE_SIZE.
+        L = lib.load()
+        n = 256 << 20
+        src, dst = hip.DeviceArray((n,), np.uint8), hip.DeviceArray((n,), np.uint8)
+        src.fill_byte(1)
+        for _ in range(5):
+            lib.check(L.kvp_probe_stream_copy(src.ptr, dst.ptr, n, 4096, None))
+        hip.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 5}))
+    else:
+        print(json.dumps(measure(), indent=1))

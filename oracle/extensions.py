@@ -199,7 +199,7 @@ def _dense(arts, dtype):
 
 def swiglu_reference(x, idx, gate, gate_arts, up_arts, down_arts):
     """fp64: out[t] = sum_s gate[t,s] * Wd_e (silu(Wg_e x_t) * (Wu_e x_t))."""
-    out = np.zeros((x.shape[0], down_arts[0].q.shape[0]), dtype=np.float64)
+    out = np.zeros((x.shape[0], down_arts[int(idx[0, 0])].q.shape[0]), dtype=np.float64)
     x64 = x.astype(np.float64)
     cache = {}
     for t in range(x.shape[0]):
@@ -218,7 +218,7 @@ def _swiglu_member(x, idx, gate, gate_arts, up_arts, down_arts, *, order="forwar
                    projection="pairwise"):
     """fp32 evaluation: projections pairwise (BLAS) or int-domain factored
     (``factored-groups``), h at fp32, slots accumulated in ``order``."""
-    out = np.zeros((x.shape[0], down_arts[0].q.shape[0]), dtype=np.float32)
+    out = np.zeros((x.shape[0], down_arts[int(idx[0, 0])].q.shape[0]), dtype=np.float32)
     x32 = x.astype(np.float32)
     slots = range(idx.shape[1]) if order == "forward" else range(idx.shape[1] - 1, -1, -1)
 
@@ -255,7 +255,7 @@ def swiglu_tolerance(dtype, x, idx, gate, gate_arts, up_arts, down_arts, ref):
 def moe_linear_reference(x, idx, gate, arts):
     """The reference's single-linear dispatch at any k, given routing:
     out[t] = sum_s gate[t,s] * (x_t @ W_e^T) in fp64 (``_moe_combine``)."""
-    out = np.zeros((x.shape[0], arts[0].q.shape[0]), dtype=np.float64)
+    out = np.zeros((x.shape[0], arts[int(idx[0, 0])].q.shape[0]), dtype=np.float64)
     dense = {}
     for t in range(x.shape[0]):
         for s in range(idx.shape[1]):
@@ -272,7 +272,7 @@ def moe_linear_tolerance(dtype, x, idx, gate, arts, ref):
     from oracle.native_ops import K_NATIVE
 
     def member(order):
-        out = np.zeros((x.shape[0], arts[0].q.shape[0]), dtype=np.float32)
+        out = np.zeros((x.shape[0], arts[int(idx[0, 0])].q.shape[0]), dtype=np.float32)
         slots = range(idx.shape[1]) if order == "f" else range(idx.shape[1] - 1, -1, -1)
         for t in range(x.shape[0]):
             for s in slots:
