@@ -376,10 +376,343 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(KvArgs a) {
 
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core split kernel (4- and 8-bit caches): one block per (slice of
+// positions, KV head, sequence); its four waves work independently on
+// 16-position tiles (tile t of the slice goes to wave t % 4), each keeping an
+// exact running-max online softmax per head, and merge once at the end.
+//
+// Scores: S[h][n] = sum_d q[h][d] * (s_n q_nd + b_n) over each 64-dim group,
+// i.e. s_n * (Q K^T)_g[h][n] + b_n * qsum_g[h]. (Q K^T)_g is a sum of
+// v_mfma_f32_16x16x32_f16 tiles: A = the query rows (heads on M, zero past
+// G), B = the tile's codes as exact fp16 denormals (a 4-bit word's eight
+// codes become four fp16 pairs with one mask split and four byte permutes),
+// fp32 accumulation. qsum_g comes from the same instruction against a B of
+// ones. The 2^24 denormal scale folds into s_n.
+// Values: a lane owns an 8-code block of a V row for every head, fp32 FMAs
+// of (p * s) * q + p * b (contract clause C1 keeps p in fp32).
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 16;  // positions per MFMA tile
+
+template <int BITS>
+__device__ __forceinline__ f16x8 codes8_f16(const uint32_t* w) {
+  // Eight codes (dims 8k .. 8k+7 of a row) as fp16 denormals, in order.
+  uint32_t h[4];
+  if constexpr (BITS == 4) {
+    const uint32_t even = w[0] & 0x0F0F0F0Fu, odd = (w[0] >> 4) & 0x0F0F0F0Fu;
+    h[0] = __builtin_amdgcn_perm(odd, even, 0x0C040C00u);
+    h[1] = __builtin_amdgcn_perm(odd, even, 0x0C050C01u);
+    h[2] = __builtin_amdgcn_perm(odd, even, 0x0C060C02u);
+    h[3] = __builtin_amdgcn_perm(odd, even, 0x0C070C03u);
+  } else {
+    h[0] = __builtin_amdgcn_perm(0u, w[0], 0x0C010C00u);
+    h[1] = __builtin_amdgcn_perm(0u, w[0], 0x0C030C02u);
+    h[2] = __builtin_amdgcn_perm(0u, w[1], 0x0C010C00u);
+    h[3] = __builtin_amdgcn_perm(0u, w[1], 0x0C030C02u);
+  }
+  f16x8 r;
+  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2_t p = __builtin_bit_cast(f16x2_t, h[i]);
+    r[2 * i] = p[0];
+    r[2 * i + 1] = p[1];
+  }
+  return r;
+}
+
+template <int BITS, int DH>
+struct MfmaTileRegs {
+  static constexpr int kKS = DH / 32;              // MFMA k-steps per row
+  static constexpr int kKW = BITS == 8 ? 2 : 1;    // words per 8 codes
+  static constexpr int kBlocks8 = DH / 8;          // V 8-code blocks per row
+  static constexpr int kVRows = kWave / kBlocks8;  // V rows per pass
+  static constexpr int kVP = kTile / kVRows;       // V passes per tile
+  uint32_t kw[kKS][kKW];
+  uint32_t ks, kb;     // fp16 scales / biases of this lane's position (1 or 2 groups)
+  uint32_t vw[kVP][kKW];
+  f16x2 vsb[kVP];
+};
+
+template <int BITS, int DH>
+__device__ __forceinline__ void load_tile(MfmaTileRegs<BITS, DH>& R, const KvArgs& a,
+                                          size_t base, int t0, int n, int lane) {
+  using TR = MfmaTileRegs<BITS, DH>;
+  constexpr int kRowWords = DH * BITS / 32;
+  constexpr int kGroups = DH / 64;
+  const int kb = lane / 16;
+  {
+    const size_t row = base + min(t0 + (lane % 16), n - 1);
+    const uint32_t* kr = a.k_wq + row * kRowWords;
+#pragma unroll
+    for (int s = 0; s < TR::kKS; ++s) {
+      if constexpr (BITS == 4) {
+        R.kw[s][0] = kr[4 * s + kb];
+      } else {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(kr + 8 * s + 2 * kb);
+        R.kw[s][0] = v.x;
+        R.kw[s][1] = v.y;
+      }
+    }
+    if constexpr (kGroups == 2) {
+      R.ks = *reinterpret_cast<const uint32_t*>(a.k_s + row * 2);
+      R.kb = *reinterpret_cast<const uint32_t*>(a.k_b + row * 2);
+    } else {
+      R.ks = a.k_s[row];
+      R.kb = a.k_b[row];
+    }
+  }
+  const int j = lane % TR::kBlocks8;
+#pragma unroll
+  for (int p = 0; p < TR::kVP; ++p) {
+    const size_t row = base + min(t0 + p * TR::kVRows + lane / TR::kBlocks8, n - 1);
+    const uint32_t* vr = a.v_wq + row * kRowWords;
+    if constexpr (BITS == 4) {
+      R.vw[p][0] = vr[j];
+    } else {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(vr + 2 * j);
+      R.vw[p][0] = v.x;
+      R.vw[p][1] = v.y;
+    }
+    const int g = (8 * j) / 64;
+    R.vsb[p] = f16x2{__builtin_bit_cast(f16, a.v_s[row * kGroups + g]),
+                     __builtin_bit_cast(f16, a.v_b[row * kGroups + g])};
+  }
+}
+
+template <int BITS, int DH, int G>
+__global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
+  using TR = MfmaTileRegs<BITS, DH>;
+  constexpr int kGroups = DH / 64;
+  constexpr int kI = 4;                   // D rows per lane
+  static_assert(G <= 8, "the value side holds 8 dims x G heads per lane");
+  __shared__ __align__(16) float pbuf[kWaves][kTile + 1][16];  // p[pos][head]; row 16: rescales
+  __shared__ float wm[kWaves][G], wl[kWaves][G];
+  __shared__ float wo[kWaves][G][DH];
+
+  const int c = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int T = min(max(a.t_cached[b], 0), a.t_stride);
+  const int slice0 = c * a.chunk;
+  if (slice0 >= T) return;  // block-uniform
+  const int n = min(a.chunk, T - slice0);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int h0 = hk * G;
+  const size_t base = ((size_t)(a.per_seq ? b : 0) * a.n_kv_heads + hk) * a.t_stride + slice0;
+  const int ntiles = (n + kTile - 1) / kTile;
+
+  // A operand: query head (lane % 16) < G, dims 32 s + 8 (lane / 16) + 0..7.
+  f16x8 qa[TR::kKS];
+  {
+    const int m = lane % 16, kb = lane / 16;
+#pragma unroll
+    for (int s = 0; s < TR::kKS; ++s) {
+      if (m < G) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + m) * DH +
+                                                         32 * s + 8 * kb);
+        qa[s] = __builtin_bit_cast(f16x8, v);
+      } else {
+        qa[s] = f16x8{};
+      }
+    }
+  }
+  // qsum per group, in the D layout (head 4 (lane / 16) + i).
+  f32x4 qsum[kGroups];
+  {
+    f16x8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones[i] = (f16)1.0f;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 2 * g; s < 2 * g + 2 && s < TR::kKS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], ones, acc, 0, 0, 0);
+      qsum[g] = acc;
+    }
+  }
+
+  float m_run[kI], l_run[kI];
+#pragma unroll
+  for (int i = 0; i < kI; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.0f;
+  }
+  float acc[G][8], pbias[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    pbias[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+  }
+
+  const int j = lane % TR::kBlocks8;
+  const float scale = a.scale * 16777216.0f;  // softmax scale x 2^24 (denormal codes)
+  float (*pw)[16] = pbuf[wave];
+
+  MfmaTileRegs<BITS, DH> A, B;
+  int tile = wave;
+  if (tile < ntiles) load_tile<BITS, DH>(A, a, base, tile * kTile, n, lane);
+
+  auto process = [&](const MfmaTileRegs<BITS, DH>& R, int t) {
+    // --- scores for the 16 positions of tile t --------------------------------
+    f32x4 d[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      f32x4 acc4 = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 2 * g; s < 2 * g + 2 && s < TR::kKS; ++s)
+        acc4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], codes8_f16<BITS>(R.kw[s]), acc4, 0,
+                                                      0, 0);
+      d[g] = acc4;
+    }
+    const bool valid = t * kTile + (lane % 16) < n;
+    float sv[kI];
+#pragma unroll
+    for (int i = 0; i < kI; ++i) {
+      float v = 0.0f;
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        const float sg = f16_bits_to_f32((uint16_t)(R.ks >> (16 * g)));
+        const float bg = f16_bits_to_f32((uint16_t)(R.kb >> (16 * g)));
+        v = fmaf(sg * scale, d[g][i], fmaf(bg * a.scale, qsum[g][i], v));
+      }
+      sv[i] = valid ? v : -INFINITY;
+    }
+    // --- online softmax over the tile (16 lanes share a head row) -------------
+    float corr[kI];
+#pragma unroll
+    for (int i = 0; i < kI; ++i) {
+      float tm = sv[i];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 16));
+      const float mn = fmaxf(m_run[i], tm);
+      corr[i] = expf(m_run[i] - mn);
+      const float p = expf(sv[i] - mn);
+      float ps = p;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 16);
+      l_run[i] = fmaf(l_run[i], corr[i], ps);
+      m_run[i] = mn;
+      sv[i] = p;
+    }
+    if (lane < 16 * ((G + 3) / 4)) {
+      *reinterpret_cast<f32x4*>(&pw[lane % 16][4 * (lane / 16)]) = f32x4{sv[0], sv[1], sv[2], sv[3]};
+      if (lane % 16 == 0)
+        *reinterpret_cast<f32x4*>(&pw[kTile][4 * (lane / 16)]) =
+            f32x4{corr[0], corr[1], corr[2], corr[3]};
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // --- values ----------------------------------------------------------------
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float cg = pw[kTile][g];
+      pbias[g] *= cg;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] *= cg;
+    }
+#pragma unroll
+    for (int p = 0; p < TR::kVP; ++p) {
+      const int r = p * TR::kVRows + lane / TR::kBlocks8;  // position in the tile
+      float codes[8];
+      if constexpr (BITS == 8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          codes[i] = (float)((R.vw[p][0] >> (8 * i)) & 0xFFu);
+          codes[4 + i] = (float)((R.vw[p][1] >> (8 * i)) & 0xFFu);
+        }
+      } else {
+        const uint32_t even = R.vw[p][0] & 0x0F0F0F0Fu, odd = (R.vw[p][0] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          codes[2 * i] = (float)((even >> (8 * i)) & 0xFFu);
+          codes[2 * i + 1] = (float)((odd >> (8 * i)) & 0xFFu);
+        }
+      }
+      const float s = (float)R.vsb[p].x, bias = (float)R.vsb[p].y;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = pw[r][g];  // 0 past the slice end (its score was -inf)
+        const float ps = pr * s;
+        pbias[g] = fmaf(pr, bias, pbias[g]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(ps, codes[i], acc[g][i]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // pbuf is rewritten by the next tile
+  };
+
+  while (tile < ntiles) {
+    const int t1 = tile + kWaves;
+    if (t1 < ntiles) load_tile<BITS, DH>(B, a, base, t1 * kTile, n, lane);
+    process(A, tile);
+    if (t1 >= ntiles) break;
+    const int t2 = t1 + kWaves;
+    if (t2 < ntiles) load_tile<BITS, DH>(A, a, base, t2 * kTile, n, lane);
+    process(B, t1);
+    tile = t2;
+  }
+
+  // --- wave results: o[g][d] summed over the lanes of a block j --------------
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = acc[g][i] + pbias[g];
+#pragma unroll
+      for (int off = TR::kBlocks8; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+      acc[g][i] = v;
+    }
+  if (lane < TR::kBlocks8) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wo[wave][g][8 * j + i] = acc[g][i];
+  }
+  // m and l of head g sit in lane 16 (g / 4), element g % 4.
+#pragma unroll
+  for (int i = 0; i < kI; ++i) {
+    const int g = 4 * (lane / 16) + i;
+    if (lane % 16 == 0 && g < G) {
+      wm[wave][g] = m_run[i];
+      wl[wave][g] = l_run[i];
+    }
+  }
+  __syncthreads();
+  // --- merge the four waves (log-sum-exp) and write the slice partial ---------
+  for (int idx = threadIdx.x; idx < G * DH; idx += kBlock) {
+    const int g = idx / DH, dd = idx - g * DH;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm[w][g]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = wl[w][g] > 0.0f ? expf(wm[w][g] - M) : 0.0f;  // idle waves hold -inf
+      L = fmaf(wl[w][g], e, L);
+      O = fmaf(wo[w][g][dd], e, O);
+    }
+    float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * a.n_chunks + c) * partial_floats(DH);
+    pp[2 + dd] = O;
+    if (dd == 0) {
+      pp[0] = M;
+      pp[1] = L;
+    }
+  }
+}
+
+bool use_mfma(int bits, int G) { return (bits == 4 || bits == 8) && G <= 8; }
+
 int pick_chunk(int bits, int batch, int n_kv_heads, int t_stride) {
   // About 1024 blocks over the longest sequence, whole 64-position steps,
-  // at most the kernel's register-bounded chunk.
-  const int cap = bits > 0 ? 128 : 128;
+  // at most the kernel's own bound (register-prefetched chunk: 128; the
+  // matrix-core kernel walks its slice tile by tile: 1024).
+  const int cap = (bits == 4 || bits == 8) ? 1024 : 128;
   long target = (long)batch * n_kv_heads * t_stride / 1024;
   int chunk = 64;
   while (chunk < cap && chunk < target) chunk *= 2;
@@ -390,8 +723,12 @@ template <int BITS, int DH, int G>
 int launch_dh_g(const KvArgs& a, int batch, hipStream_t st) {
   if (a.t_stride > 0) {
     const dim3 grid(a.n_chunks, a.n_kv_heads, batch);
-    const size_t lds = (size_t)G * a.chunk * sizeof(float);
-    hipLaunchKernelGGL((kv_split_kernel<BITS, DH, G>), grid, dim3(kBlock), lds, st, a);
+    if constexpr ((BITS == 4 || BITS == 8) && G <= 8) {
+      hipLaunchKernelGGL((kv_mfma_split_kernel<BITS, DH, G>), grid, dim3(kBlock), 0, st, a);
+    } else {
+      const size_t lds = (size_t)G * a.chunk * sizeof(float);
+      hipLaunchKernelGGL((kv_split_kernel<BITS, DH, G>), grid, dim3(kBlock), lds, st, a);
+    }
     const int rc = check_launch("kvp_kv_decode (split)");
     if (rc != KVP_OK) return rc;
   }
@@ -416,7 +753,7 @@ int launch_dh(int G, const KvArgs& a, int batch, hipStream_t st) {
 
 template <int BITS>
 int launch_bits(int dh, int G, const KvArgs& a, int batch, hipStream_t st) {
-  if (a.chunk > max_chunk<BITS>())
+  if (!use_mfma(BITS, G) && a.chunk > max_chunk<BITS>())
     return set_error(KVP_INVALID, "kvp_kv_decode: chunk=%d above %d at %d bits", a.chunk,
                      max_chunk<BITS>(), BITS);
   if (dh == 64) return launch_dh<BITS, 64>(G, a, batch, st);

@@ -40,19 +40,26 @@ def should_dispatch(t: int) -> bool:
     return t >= 0
 
 
-def max_chunk(bits: int) -> int:
-    """Largest chunk a block takes (its prefetched codes live in registers)."""
-    return 128
+def uses_matrix_cores(bits: int, gqa: int) -> bool:
+    """4- and 8-bit caches with up to 8 query heads per KV head take the
+    MFMA score kernel; 2- and 3-bit caches the all-VALU kernel."""
+    return bits in (4, 8) and gqa <= 8
+
+
+def max_chunk(bits: int, gqa: int = 4) -> int:
+    """Largest chunk (positions per block): the MFMA kernel walks its slice
+    tile by tile; the VALU kernel holds its chunk's codes in registers."""
+    return 1024 if uses_matrix_cores(bits, gqa) else 128
 
 
 def launch_config(batch: int, n_kv_heads: int, t_stride: int, bits: int = 4,
-                  chunk: int | None = None):
+                  chunk: int | None = None, gqa: int = 4):
     """(grid, block, chunk): one block per (chunk, KV head, sequence); the
     library's own chunk choice (about 1024 blocks) when ``chunk`` is None."""
     if not chunk:
         target = batch * n_kv_heads * t_stride // 1024
         chunk = 64
-        while chunk < max_chunk(bits) and chunk < target:
+        while chunk < max_chunk(bits, gqa) and chunk < target:
             chunk *= 2
     n_chunks = max(1, -(-t_stride // chunk))
     return (n_chunks, n_kv_heads, batch), (256, 1, 1), chunk
@@ -123,7 +130,7 @@ class KvDecodeCall:
             raise lib.InvalidArgument("kv_decode: t_cached must be int32 (B,)")
         if out.shape != (b, h, dh) or out.dtype.name not in OUT_DTYPES:
             raise lib.InvalidArgument(f"kv_decode: out must be fp16/fp32 {(b, h, dh)}")
-        _, _, chunk = launch_config(b, hkv, t_stride, bits, chunk or None)
+        _, _, chunk = launch_config(b, hkv, t_stride, bits, chunk or None, gqa=h // hkv)
         need = workspace_bytes(b, h, dh, t_stride, chunk)
         if workspace is None:
             workspace = DeviceArray((max(need, 4),), np.uint8)
