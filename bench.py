@@ -106,7 +106,7 @@ class KvWorkload:
     (``kvp_quantize_affine``), rotated over >= 1 GiB of device copies."""
 
     def __init__(self, lengths, n_heads=32, n_kv_heads=8, head_dim=128, bits=4,
-                 per_sequence=False, t_stride=None, seed=0):
+                 per_sequence=False, t_stride=None, seed=0, chunk=None):
         from kernelverify_amd import hip
         from kernelverify_amd.hip import DeviceArray
         from kernelverify_amd.pack import kv_attention
@@ -145,7 +145,8 @@ class KvWorkload:
             parts = [a if i == 0 else DeviceArray.from_host(a.to_host()) for a in (*k, *v)]
             call = kv_attention.KvDecodeCall(self.dq, *parts[:3], *parts[3:], self.dnk, self.dnv,
                                              self.dt, self.out, bits=bits,
-                                             cache_per_sequence=per_sequence, workspace=ws)
+                                             cache_per_sequence=per_sequence, workspace=ws,
+                                             chunk=chunk or 0)
             ws = call.workspace
             self.calls.append(call)
         self.i = 0

@@ -25,7 +25,9 @@
 //
 // This is the online-softmax tiling of contract clause C3
 // (kernelverify/tolerance/contract.py:31-46): exact in exact arithmetic,
-// every intermediate fp32, exp via the accurate expf.
+// every intermediate fp32. The softmax runs in base 2: scores carry
+// log2(e) / sqrt(DH) (one rounding), so e^(s-m) is exp2 of the scaled
+// difference; the partials' m is in the same base-2 units.
 //
 // Score side: a lane owns one unit (16 bytes; 24 for 3-bit) of a K row, so a
 // wave's K load instruction covers 64/U whole rows contiguously. The lane's
@@ -38,6 +40,8 @@
 // block, kv_attention.py:194-217) for every G head, accumulating
 // (p * s) * q + p * b in fp32.
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.h"
 #include "qmv_core.h"
@@ -66,11 +70,11 @@ struct KvArgs {
   const f16* new_k;
   const f16* new_v;
   const int32_t* t_cached;
-  float* part;           // [B][H][n_chunks][2 + DH] per-chunk (m, l, o)
+  float* part;           // [B][H][n_chunks][2 + DH] per-chunk (m, l, o), m in base-2 units
   void* out;
   int out_f32;
   int n_heads, n_kv_heads, t_stride, chunk, n_chunks, per_seq;
-  float scale;
+  float scale;           // log2(e) / sqrt(DH)
 };
 
 // The 8-code block j of a row (codes 8j .. 8j+7) as the low 8*BITS bits of
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
 #pragma unroll 8
   for (int c = grp; c < nc; c += kCombGroups) {
     const float* pc = pz + c * partial_floats(DH);
-    const float e = expf(pc[0] - M);
+    const float e = exp2f(pc[0] - M);
     o = fmaf(pc[2 + d0 + dd], e, o);
     l = fmaf(pc[1], e, l);
   }
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
   if (dd == 0) lsum[grp] = l;
   __syncthreads();
   if (threadIdx.x < kCombDims) {
-    const float e_new = expf(s_new_sh - M);
+    const float e_new = exp2f(s_new_sh - M);
     const f16* nv = a.new_v + ((size_t)b * a.n_kv_heads + hk) * DH;
     float v = e_new * (float)nv[d0 + dd];
     float L = e_new;
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(KvArgs a) {
       const float m = stat_m[g];
       float l = 0.0f;
       for (int t = threadIdx.x; t < n; t += kBlock) {
-        const float e = expf(sc[g * a.chunk + t] - m);
+        const float e = exp2f(sc[g * a.chunk + t] - m);
         sc[g * a.chunk + t] = e;
         l += e;
       }
@@ -377,25 +381,40 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(KvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core split kernel (4- and 8-bit caches): one block per (slice of
-// positions, KV head, sequence); its four waves work independently on
-// 16-position tiles (tile t of the slice goes to wave t % 4), each keeping an
-// exact running-max online softmax per head, and merge once at the end.
+// Matrix-core split kernel (4- and 8-bit caches, G <= 8 query heads per KV
+// head): one block per (slice of positions, KV head, sequence). Its four
+// waves work independently on 32-position steps (step t of the slice goes to
+// wave t % 4), each keeping an exact running-max online softmax per head in
+// the base-2 domain, and merge once at the end.
 //
-// Scores: S[h][n] = sum_d q[h][d] * (s_n q_nd + b_n) over each 64-dim group,
-// i.e. s_n * (Q K^T)_g[h][n] + b_n * qsum_g[h]. (Q K^T)_g is a sum of
-// v_mfma_f32_16x16x32_f16 tiles: A = the query rows (heads on M, zero past
-// G), B = the tile's codes as exact fp16 denormals (a 4-bit word's eight
-// codes become four fp16 pairs with one mask split and four byte permutes),
-// fp32 accumulation. qsum_g comes from the same instruction against a B of
-// ones. The 2^24 denormal scale folds into s_n.
-// Values: a lane owns an 8-code block of a V row for every head, fp32 FMAs
-// of (p * s) * q + p * b (contract clause C1 keeps p in fp32).
+// Scores, two 16-position tiles per step:
+//   S[h][n] = sum_g s_n,g (Q K_g^T)[h][n] + b_n,g qsum_g[h]
+// over the 64-dim groups g. (Q K_g^T) is a sum of v_mfma_f32_16x16x32_f16:
+// A = the query rows (heads on M, zero past G), B = the codes as exact fp16
+// denormals (c -> c * 2^-24, folded into the score scale), fp32
+// accumulation; qsum_g comes from the same instruction against ones.
+//
+// Values, one v_mfma_f32_16x16x32_f16 per 16 dims over the step's 32
+// positions:
+//   O[h][d] = sum_n p[h][n] s_n,g(d) c[n][d] + sum_n p[h][n] b_n,g(d).
+// The first sum runs on the matrix cores: B = the codes (exact fp16
+// denormals), A = x = p * s * 2^E carried as an unevaluated sum of two fp16
+// values, hi = rne(x) and lo = rne(x - hi) (22 significant bits; every
+// product exact; fp32 accumulation). The 16 rows of A are the pairs
+// (group, hi/lo, head), so one instruction serves every head and both
+// parts; the two parts are added once at the end. E is a power-of-two range
+// shift per group chosen from the largest V scale seen so far so that
+// x < 2^15; a larger scale later lowers E and rescales the accumulators by
+// the exact power of two. The second sum (p * b) stays on the VALU in fp32.
+// A lane of the value instruction owns one code word of a V row (its column
+// of 16 dims) at 8 consecutive positions (its K-rows).
 // ---------------------------------------------------------------------------
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTile = 16;  // positions per MFMA tile
+constexpr int kTile = 16;  // positions per score tile
+constexpr int kStep = 32;  // positions per wave step: two score tiles, one value block
 
 template <int BITS>
 __device__ __forceinline__ f16x8 codes8_f16(const uint32_t* w) {
@@ -413,83 +432,161 @@ __device__ __forceinline__ f16x8 codes8_f16(const uint32_t* w) {
     h[2] = __builtin_amdgcn_perm(0u, w[1], 0x0C010C00u);
     h[3] = __builtin_amdgcn_perm(0u, w[1], 0x0C030C02u);
   }
-  f16x8 r;
-  typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f16x2_t p = __builtin_bit_cast(f16x2_t, h[i]);
-    r[2 * i] = p[0];
-    r[2 * i + 1] = p[1];
-  }
-  return r;
+  return __builtin_bit_cast(f16x8, u32x4{h[0], h[1], h[2], h[3]});
+}
+
+// Reductions over the 16 lanes of a DPP row; every lane of the row gets the
+// same (bit-identical) result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141;  // row_half_mirror
+constexpr int kRowMirror = 0x140;   // row_mirror
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kQuadSwap1>(v));
+  v = fmaxf(v, dpp_f<kQuadSwap2>(v));
+  v = fmaxf(v, dpp_f<kHalfMirror>(v));
+  return fmaxf(v, dpp_f<kRowMirror>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kQuadSwap1>(v);
+  v += dpp_f<kQuadSwap2>(v);
+  v += dpp_f<kHalfMirror>(v);
+  return v + dpp_f<kRowMirror>(v);
+}
+__device__ __forceinline__ int row16_max_i(int v) {
+  v = max(v, dpp_i<kQuadSwap1>(v));
+  v = max(v, dpp_i<kQuadSwap2>(v));
+  v = max(v, dpp_i<kHalfMirror>(v));
+  return max(v, dpp_i<kRowMirror>(v));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+// 2^e as a float for -126 <= e <= 127; 0 below.
+__device__ __forceinline__ float exp2_int(int e) {
+  return e < -126 ? 0.0f : __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
 }
 
 template <int BITS, int DH>
-struct MfmaTileRegs {
-  static constexpr int kKS = DH / 32;              // MFMA k-steps per row
-  static constexpr int kKW = BITS == 8 ? 2 : 1;    // words per 8 codes
-  static constexpr int kBlocks8 = DH / 8;          // V 8-code blocks per row
-  static constexpr int kVRows = kWave / kBlocks8;  // V rows per pass
-  static constexpr int kVP = kTile / kVRows;       // V passes per tile
-  uint32_t kw[kKS][kKW];
-  uint32_t ks, kb;     // fp16 scales / biases of this lane's position (1 or 2 groups)
-  uint32_t vw[kVP][kKW];
-  f16x2 vsb[kVP];
+struct KvStepShape {
+  static constexpr int kKS = DH / 32;                          // score k-steps per row
+  static constexpr int kKW = BITS == 8 ? 2 : 1;                // words per 8 codes
+  static constexpr int kGroups = DH / 64;
+  static constexpr int kRowWords = DH * BITS / 32;
+  static constexpr int kVW = (BITS == 8 && DH == 128) ? 2 : 1;  // V words per lane and position
+  static constexpr int kNB = DH / 16;                          // value instructions per row set
+  static constexpr int kHR = DH == 128 ? 4 : 8;                // heads per row set
+};
+
+// What a lane loads for one step.
+template <int BITS, int DH>
+struct KvStepRegs {
+  using S = KvStepShape<BITS, DH>;
+  uint32_t kw[2][S::kKS][S::kKW];  // K codes: tile, k-step (lane's position n16, dims 32s+8kb..)
+  uint32_t ks[2], kbias[2];        // K scales / biases at the lane's score position (groups packed)
+  uint32_t vs[2], vbias[2];        // V scales / biases at the lane's score position
+  uint32_t vw[8][S::kVW];          // V codes: positions 8 kb + j, the lane's column word
 };
 
 template <int BITS, int DH>
-__device__ __forceinline__ void load_tile(MfmaTileRegs<BITS, DH>& R, const KvArgs& a,
-                                          size_t base, int t0, int n, int lane) {
-  using TR = MfmaTileRegs<BITS, DH>;
-  constexpr int kRowWords = DH * BITS / 32;
-  constexpr int kGroups = DH / 64;
-  const int kb = lane / 16;
-  {
-    const size_t row = base + min(t0 + (lane % 16), n - 1);
-    const uint32_t* kr = a.k_wq + row * kRowWords;
+__device__ __forceinline__ void load_step(KvStepRegs<BITS, DH>& R, const KvArgs& a, size_t base,
+                                          int p0, int n, int lane) {
+  using S = KvStepShape<BITS, DH>;
+  const int n16 = lane % 16, kb = lane / 16;
 #pragma unroll
-    for (int s = 0; s < TR::kKS; ++s) {
+  for (int tt = 0; tt < 2; ++tt) {
+    const size_t row = base + min(p0 + kTile * tt + n16, n - 1);
+    const uint32_t* kr = a.k_wq + row * S::kRowWords;
+#pragma unroll
+    for (int s = 0; s < S::kKS; ++s) {
       if constexpr (BITS == 4) {
-        R.kw[s][0] = kr[4 * s + kb];
+        R.kw[tt][s][0] = kr[4 * s + kb];
       } else {
         const u32x2 v = *reinterpret_cast<const u32x2*>(kr + 8 * s + 2 * kb);
-        R.kw[s][0] = v.x;
-        R.kw[s][1] = v.y;
+        R.kw[tt][s][0] = v.x;
+        R.kw[tt][s][1] = v.y;
       }
     }
-    if constexpr (kGroups == 2) {
-      R.ks = *reinterpret_cast<const uint32_t*>(a.k_s + row * 2);
-      R.kb = *reinterpret_cast<const uint32_t*>(a.k_b + row * 2);
+    if constexpr (S::kGroups == 2) {
+      R.ks[tt] = *reinterpret_cast<const uint32_t*>(a.k_s + row * 2);
+      R.kbias[tt] = *reinterpret_cast<const uint32_t*>(a.k_b + row * 2);
+      R.vs[tt] = *reinterpret_cast<const uint32_t*>(a.v_s + row * 2);
+      R.vbias[tt] = *reinterpret_cast<const uint32_t*>(a.v_b + row * 2);
     } else {
-      R.ks = a.k_s[row];
-      R.kb = a.k_b[row];
+      R.ks[tt] = a.k_s[row];
+      R.kbias[tt] = a.k_b[row];
+      R.vs[tt] = a.v_s[row];
+      R.vbias[tt] = a.v_b[row];
     }
   }
-  const int j = lane % TR::kBlocks8;
+  // The lane's column word: 4-bit DH 128 word n16 (dims 8 n16 ..), 8-bit
+  // DH 128 words 2 n16, 2 n16 + 1 (dims 8 n16 ..), 4-bit DH 64 word n16 % 8,
+  // 8-bit DH 64 word n16 (dims 4 n16 ..).
+  const int col = (BITS == 4 && DH == 64) ? n16 % 8 : n16;
 #pragma unroll
-  for (int p = 0; p < TR::kVP; ++p) {
-    const size_t row = base + min(t0 + p * TR::kVRows + lane / TR::kBlocks8, n - 1);
-    const uint32_t* vr = a.v_wq + row * kRowWords;
-    if constexpr (BITS == 4) {
-      R.vw[p][0] = vr[j];
+  for (int j = 0; j < 8; ++j) {
+    const size_t row = base + min(p0 + 8 * kb + j, n - 1);
+    const uint32_t* vr = a.v_wq + row * S::kRowWords;
+    if constexpr (S::kVW == 2) {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(vr + 2 * col);
+      R.vw[j][0] = v.x;
+      R.vw[j][1] = v.y;
     } else {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(vr + 2 * j);
-      R.vw[p][0] = v.x;
-      R.vw[p][1] = v.y;
+      R.vw[j][0] = vr[col];
     }
-    const int g = (8 * j) / 64;
-    R.vsb[p] = f16x2{__builtin_bit_cast(f16, a.v_s[row * kGroups + g]),
-                     __builtin_bit_cast(f16, a.v_b[row * kGroups + g])};
   }
+}
+
+// Dim of code `nb` in column n16 of the value instruction.
+template <int BITS, int DH>
+__device__ __forceinline__ int value_dim(int n16, int nb) {
+  if constexpr (DH == 128) return 8 * n16 + nb;
+  else if constexpr (BITS == 4) return 8 * (n16 % 8) + 4 * (n16 / 8) + nb;
+  else return 4 * n16 + nb;
+}
+
+// B operand of value instruction nb: element j = code nb of the lane's
+// column at position 8 kb + j, as an fp16 denormal. `pl` holds the 4-bit
+// nibble planes (even, odd) or the 8-bit words.
+template <int BITS, int DH, int NB>
+__device__ __forceinline__ f16x8 value_codes(const uint32_t (&pl)[8][2]) {
+  uint32_t h[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    if constexpr (BITS == 4) {
+      constexpr int k = NB >> 1;  // byte of the plane
+      constexpr uint32_t sel = 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k;
+      h[p] = __builtin_amdgcn_perm(pl[2 * p + 1][NB & 1], pl[2 * p][NB & 1], sel);
+    } else {
+      constexpr int k = NB & 3;
+      constexpr uint32_t sel = 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k;
+      h[p] = __builtin_amdgcn_perm(pl[2 * p + 1][NB >> 2], pl[2 * p][NB >> 2], sel);
+    }
+  }
+  return __builtin_bit_cast(f16x8, u32x4{h[0], h[1], h[2], h[3]});
 }
 
 template <int BITS, int DH, int G>
 __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
-  using TR = MfmaTileRegs<BITS, DH>;
-  constexpr int kGroups = DH / 64;
-  constexpr int kI = 4;                   // D rows per lane
-  static_assert(G <= 8, "the value side holds 8 dims x G heads per lane");
-  __shared__ __align__(16) float pbuf[kWaves][kTile + 1][16];  // p[pos][head]; row 16: rescales
+  using S = KvStepShape<BITS, DH>;
+  constexpr int kGroups = S::kGroups;
+  constexpr int kHR = S::kHR;
+  constexpr int kSets = (G + kHR - 1) / kHR;      // value row sets
+  constexpr int kHp = G <= 4 ? 4 : 8;             // heads per LDS position row (padded)
+  constexpr int kXS = kGroups * kHp;              // floats per position in xbuf
+  constexpr int kXWave = kStep * kXS + 4 * 8;     // + 8 floats per 8 positions (bank spread)
+  static_assert(G <= 8, "at most 8 query heads per KV head");
+  __shared__ __align__(16) float xbuf[kWaves][kXWave];
   __shared__ float wm[kWaves][G], wl[kWaves][G];
   __shared__ float wo[kWaves][G][DH];
 
@@ -500,191 +597,320 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   const int n = min(a.chunk, T - slice0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
+  const int n16 = lane % 16, q4 = lane / 16;
   const int h0 = hk * G;
   const size_t base = ((size_t)(a.per_seq ? b : 0) * a.n_kv_heads + hk) * a.t_stride + slice0;
-  const int ntiles = (n + kTile - 1) / kTile;
+  const int nsteps = (n + kStep - 1) / kStep;
+  float* xw = xbuf[wave];
+  auto xaddr = [](int pos, int g, int h) { return pos * kXS + (pos / 8) * 8 + g * kHp + h; };
 
-  // A operand: query head (lane % 16) < G, dims 32 s + 8 (lane / 16) + 0..7.
-  f16x8 qa[TR::kKS];
-  {
-    const int m = lane % 16, kb = lane / 16;
+  // Score A operand: query head n16 < G, dims 32 s + 8 q4 + 0..7.
+  f16x8 qa[S::kKS];
 #pragma unroll
-    for (int s = 0; s < TR::kKS; ++s) {
-      if (m < G) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + m) * DH +
-                                                         32 * s + 8 * kb);
-        qa[s] = __builtin_bit_cast(f16x8, v);
-      } else {
-        qa[s] = f16x8{};
-      }
+  for (int s = 0; s < S::kKS; ++s) {
+    if (n16 < G) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + n16) * DH +
+                                                       32 * s + 8 * q4);
+      qa[s] = __builtin_bit_cast(f16x8, v);
+    } else {
+      qa[s] = f16x8{};
     }
   }
-  // qsum per group, in the D layout (head 4 (lane / 16) + i).
+
+  KvStepRegs<BITS, DH> RA, RB;
+  if (wave < nsteps) load_step<BITS, DH>(RA, a, base, kStep * wave, n, lane);
+
+  // qsum per group in the score layout (head 4 q4 + i).
   f32x4 qsum[kGroups];
   {
     f16x8 ones;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ones[i] = (f16)1.0f;
+    for (int i = 0; i < 8; ++i) ones[i] = (_Float16)1.0f;
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) {
       f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-      for (int s = 2 * g; s < 2 * g + 2 && s < TR::kKS; ++s)
+      for (int s = 2 * g; s < 2 * g + 2; ++s)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], ones, acc, 0, 0, 0);
       qsum[g] = acc;
     }
   }
 
-  float m_run[kI], l_run[kI];
+  // Running state. m: per head, wave-uniform (base-2 units). l, pb: per
+  // lane partial sums in the score layout, reduced over the row at the end.
+  // mrow[i]: running max of head 4 q4 + i, the heads of this lane's score
+  // row (uniform over the row; rows past the last real head hold scores of
+  // zero query rows and are never read).
+  float mrow[4];
 #pragma unroll
-  for (int i = 0; i < kI; ++i) {
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.0f;
+  for (int i = 0; i < 4; ++i) mrow[i] = -INFINITY;
+  float l[4], pb[4][kGroups];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    l[i] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) pb[i][g] = 0.0f;
   }
-  float acc[G][8], pbias[G];
+  f32x4 acc[kSets][S::kNB];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    pbias[g] = 0.0f;
+  for (int st = 0; st < kSets; ++st)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
-  }
+    for (int nb = 0; nb < S::kNB; ++nb) acc[st][nb] = f32x4{0, 0, 0, 0};
+  int E[kGroups];        // range shift per group (uniform); 127 = no nonzero scale yet
+  uint32_t thr = 0;      // per 16-bit half: largest |V scale| bits that fit the current E
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) E[g] = 127;
 
-  const int j = lane % TR::kBlocks8;
-  const float scale = a.scale * 16777216.0f;  // softmax scale x 2^24 (denormal codes)
-  float (*pw)[16] = pbuf[wave];
+  const float scale24 = a.scale * 16777216.0f;  // base-2 softmax scale x 2^24 (denormal codes)
+  // Value A operand row of this lane: (group, hi/lo part, head).
+  const int g_r = DH == 128 ? n16 >> 3 : 0;
+  const int hl_r = DH == 128 ? (n16 & 3) : (n16 & 7);
+  const float lo_r = (DH == 128 ? (n16 >> 2) & 1 : n16 >> 3) ? 1.0f : 0.0f;
 
-  MfmaTileRegs<BITS, DH> A, B;
-  int tile = wave;
-  if (tile < ntiles) load_tile<BITS, DH>(A, a, base, tile * kTile, n, lane);
-
-  auto process = [&](const MfmaTileRegs<BITS, DH>& R, int t) {
-    // --- scores for the 16 positions of tile t --------------------------------
-    f32x4 d[kGroups];
+  auto process = [&](const KvStepRegs<BITS, DH>& R, int t) {
+    const int p0 = kStep * t;
+    // --- scores of the two tiles ---------------------------------------------
+    float sv[2][4];
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      f32x4 acc4 = {0, 0, 0, 0};
-#pragma unroll
-      for (int s = 2 * g; s < 2 * g + 2 && s < TR::kKS; ++s)
-        acc4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], codes8_f16<BITS>(R.kw[s]), acc4, 0,
-                                                      0, 0);
-      d[g] = acc4;
-    }
-    const bool valid = t * kTile + (lane % 16) < n;
-    float sv[kI];
-#pragma unroll
-    for (int i = 0; i < kI; ++i) {
-      float v = 0.0f;
+    for (int tt = 0; tt < 2; ++tt) {
+      f32x4 d[kGroups];
 #pragma unroll
       for (int g = 0; g < kGroups; ++g) {
-        const float sg = f16_bits_to_f32((uint16_t)(R.ks >> (16 * g)));
-        const float bg = f16_bits_to_f32((uint16_t)(R.kb >> (16 * g)));
-        v = fmaf(sg * scale, d[g][i], fmaf(bg * a.scale, qsum[g][i], v));
+        f32x4 a4 = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 2 * g; s < 2 * g + 2; ++s)
+          a4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], codes8_f16<BITS>(R.kw[tt][s]), a4, 0,
+                                                      0, 0);
+        d[g] = a4;
       }
-      sv[i] = valid ? v : -INFINITY;
+      const bool valid = p0 + kTile * tt + n16 < n;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+          const float sg = f16_bits_to_f32((uint16_t)(R.ks[tt] >> (16 * g)));
+          const float bg = f16_bits_to_f32((uint16_t)(R.kbias[tt] >> (16 * g)));
+          v = fmaf(sg * scale24, d[g][i], fmaf(bg * a.scale, qsum[g][i], v));
+        }
+        sv[tt][i] = valid ? v : -INFINITY;
+      }
     }
-    // --- online softmax over the tile (16 lanes share a head row) -------------
-    float corr[kI];
+    // --- running max per head (uniform), probabilities --------------------------
+    float mx[4];
 #pragma unroll
-    for (int i = 0; i < kI; ++i) {
-      float tm = sv[i];
+    for (int i = 0; i < 4; ++i) mx[i] = row16_max(fmaxf(sv[0][i], sv[1][i]));
+    float csel[4];
+    bool grew_lane = false;
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 16));
-      const float mn = fmaxf(m_run[i], tm);
-      corr[i] = expf(m_run[i] - mn);
-      const float p = expf(sv[i] - mn);
-      float ps = p;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 16);
-      l_run[i] = fmaf(l_run[i], corr[i], ps);
-      m_run[i] = mn;
-      sv[i] = p;
+    for (int i = 0; i < 4; ++i) {
+      const float mn = fmaxf(mrow[i], mx[i]);
+      csel[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);
+      grew_lane |= mn > mrow[i];
+      mrow[i] = mn;
     }
-    if (lane < 16 * ((G + 3) / 4)) {
-      *reinterpret_cast<f32x4*>(&pw[lane % 16][4 * (lane / 16)]) = f32x4{sv[0], sv[1], sv[2], sv[3]};
-      if (lane % 16 == 0)
-        *reinterpret_cast<f32x4*>(&pw[kTile][4 * (lane / 16)]) =
-            f32x4{corr[0], corr[1], corr[2], corr[3]};
+    const bool grew = __builtin_amdgcn_ballot_w64(grew_lane) != 0;  // wave-uniform
+    float p[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - mrow[i]);
+
+    // --- range shift: a V scale larger than the current E admits -----------------
+    const uint32_t ub = __builtin_bit_cast(
+        uint32_t, __builtin_elementwise_max(
+                      __builtin_bit_cast(u16x2, R.vs[0] & 0x7FFF7FFFu),
+                      __builtin_bit_cast(u16x2, R.vs[1] & 0x7FFF7FFFu)));
+    const bool over = __builtin_bit_cast(uint32_t,
+                                         __builtin_elementwise_max(__builtin_bit_cast(u16x2, ub),
+                                                                   __builtin_bit_cast(u16x2, thr))) != thr;
+    float fE0 = 1.0f, fE1 = 1.0f;  // accumulator rescale of groups 0 / 1
+    bool shifted = false;
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {  // wave-uniform, rare
+      uint32_t nthr = 0;
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        const int e = __builtin_amdgcn_readlane(row16_max_i((int)((ub >> (16 * g)) & 0xFFFFu)), 0) >> 10;
+        const int en = min(E[g], 29 - e);
+        (g ? fE1 : fE0) = exp2_int(en - E[g]);
+        shifted |= en != E[g];
+        E[g] = en;
+        nthr |= (uint32_t)(((30 - en) << 10) - 1) << (16 * g);
+      }
+      thr = nthr;
+    }
+    if (grew || shifted) {  // wave-uniform
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        l[i] *= csel[i];
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) pb[i][g] *= csel[i];
+      }
+      // value accumulator rows of this lane: group, head 4 q4 + i (row set st)
+#pragma unroll
+      for (int st = 0; st < kSets; ++st) {
+        float f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (DH == 128) {
+            // row set st holds heads 4 st + i (score row st); the lane's group is q4 / 2
+            f[i] = lane_value(csel[i], 16 * st) * ((q4 >> 1) ? fE1 : fE0);
+          } else {
+            // heads 4 (q4 % 2) + i (score row q4 % 2)
+            const float c0 = lane_value(csel[i], 0), c1 = lane_value(csel[i], 16);
+            f[i] = ((q4 & 1) ? c1 : c0) * fE0;
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < S::kNB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[st][nb][i] *= f[i];
+      }
+    }
+    float sE[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) sE[g] = exp2_int(E[g]);
+    // --- l, p * b, and x = p * s * 2^E into LDS (position, group, head) ---------
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      float x[kGroups][4];
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        const float vsg = f16_bits_to_f32((uint16_t)(R.vs[tt] >> (16 * g))) * sE[g];
+        const float vbg = f16_bits_to_f32((uint16_t)(R.vbias[tt] >> (16 * g)));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[g][i] = p[tt][i] * vsg;
+          pb[i][g] = fmaf(p[tt][i], vbg, pb[i][g]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) l[i] += p[tt][i];
+      if (q4 < (G + 3) / 4) {
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+          *reinterpret_cast<f32x4*>(&xw[xaddr(kTile * tt + n16, g, 4 * q4)]) =
+              f32x4{x[g][0], x[g][1], x[g][2], x[g][3]};
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // --- values ----------------------------------------------------------------
+    // --- values on the matrix cores ---------------------------------------------
+    uint32_t pl[8][2];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float cg = pw[kTile][g];
-      pbias[g] *= cg;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] *= cg;
-    }
-#pragma unroll
-    for (int p = 0; p < TR::kVP; ++p) {
-      const int r = p * TR::kVRows + lane / TR::kBlocks8;  // position in the tile
-      float codes[8];
-      if constexpr (BITS == 8) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          codes[i] = (float)((R.vw[p][0] >> (8 * i)) & 0xFFu);
-          codes[4 + i] = (float)((R.vw[p][1] >> (8 * i)) & 0xFFu);
-        }
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (BITS == 4) {
+        const uint32_t w = DH == 64 ? (n16 >= 8 ? R.vw[j][0] >> 16 : R.vw[j][0]) : R.vw[j][0];
+        pl[j][0] = w & 0x0F0F0F0Fu;
+        pl[j][1] = (w >> 4) & 0x0F0F0F0Fu;
       } else {
-        const uint32_t even = R.vw[p][0] & 0x0F0F0F0Fu, odd = (R.vw[p][0] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          codes[2 * i] = (float)((even >> (8 * i)) & 0xFFu);
-          codes[2 * i + 1] = (float)((odd >> (8 * i)) & 0xFFu);
-        }
-      }
-      const float s = (float)R.vsb[p].x, bias = (float)R.vsb[p].y;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pr = pw[r][g];  // 0 past the slice end (its score was -inf)
-        const float ps = pr * s;
-        pbias[g] = fmaf(pr, bias, pbias[g]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(ps, codes[i], acc[g][i]);
+        pl[j][0] = R.vw[j][0];
+        pl[j][1] = S::kVW == 2 ? R.vw[j][S::kVW - 1] : 0u;
       }
     }
-    __builtin_amdgcn_wave_barrier();  // pbuf is rewritten by the next tile
+#pragma unroll
+    for (int st = 0; st < kSets; ++st) {
+      const int h = min(kHR * st + hl_r, G - 1);  // rows past G repeat a real head
+      f16x8 av;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv = xw[xaddr(8 * q4 + j, g_r, h)];
+        const _Float16 hi = (_Float16)xv;
+        av[j] = (_Float16)fmaf(-lo_r, (float)hi, xv);
+      }
+      auto mm = [&](auto nbc) {
+        constexpr int NB = decltype(nbc)::value;
+        acc[st][NB] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, value_codes<BITS, DH, NB>(pl),
+                                                            acc[st][NB], 0, 0, 0);
+      };
+      mm(std::integral_constant<int, 0>{});
+      mm(std::integral_constant<int, 1>{});
+      mm(std::integral_constant<int, 2>{});
+      mm(std::integral_constant<int, 3>{});
+      if constexpr (S::kNB == 8) {
+        mm(std::integral_constant<int, 4>{});
+        mm(std::integral_constant<int, 5>{});
+        mm(std::integral_constant<int, 6>{});
+        mm(std::integral_constant<int, 7>{});
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // xbuf is rewritten by the next step
   };
 
-  while (tile < ntiles) {
-    const int t1 = tile + kWaves;
-    if (t1 < ntiles) load_tile<BITS, DH>(B, a, base, t1 * kTile, n, lane);
-    process(A, tile);
-    if (t1 >= ntiles) break;
-    const int t2 = t1 + kWaves;
-    if (t2 < ntiles) load_tile<BITS, DH>(A, a, base, t2 * kTile, n, lane);
-    process(B, t1);
-    tile = t2;
+  if (wave < nsteps) {
+    // Double-buffered: the next step's loads are issued before this step's
+    // work, unconditionally (past the end they repeat the last step), so the
+    // wait before each step covers exactly the older set.
+    int t = wave;
+    const int last = nsteps - 1;
+    for (;;) {
+      load_step<BITS, DH>(RB, a, base, kStep * min(t + kWaves, last), n, lane);
+      process(RA, t);
+      t += kWaves;
+      if (t > last) break;
+      load_step<BITS, DH>(RA, a, base, kStep * min(t + kWaves, last), n, lane);
+      process(RB, t);
+      t += kWaves;
+      if (t > last) break;
+    }
   }
 
-  // --- wave results: o[g][d] summed over the lanes of a block j --------------
+  // --- wave results ---------------------------------------------------------------
+  // Row sums of l and p * b, uniform per head: heads 0-3 from row 0, 4-7 from row 1.
+  f32x4 lA, lB, pA0, pA1, pB0, pB1;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = acc[g][i] + pbias[g];
-#pragma unroll
-      for (int off = TR::kBlocks8; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
-      acc[g][i] = v;
-    }
-  if (lane < TR::kBlocks8) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) wo[wave][g][8 * j + i] = acc[g][i];
+  for (int i = 0; i < 4; ++i) {
+    const float ls = row16_sum(l[i]);
+    const float p0 = row16_sum(pb[i][0]);
+    const float p1 = row16_sum(pb[i][kGroups - 1]);
+    lA[i] = lane_value(ls, 0);
+    lB[i] = lane_value(ls, 16);
+    pA0[i] = lane_value(p0, 0);
+    pB0[i] = lane_value(p0, 16);
+    pA1[i] = lane_value(p1, 0);
+    pB1[i] = lane_value(p1, 16);
   }
-  // m and l of head g sit in lane 16 (g / 4), element g % 4.
+  const float inv0 = exp2_int(24 - E[0]), inv1 = exp2_int(24 - E[kGroups - 1]);
 #pragma unroll
-  for (int i = 0; i < kI; ++i) {
-    const int g = 4 * (lane / 16) + i;
-    if (lane % 16 == 0 && g < G) {
-      wm[wave][g] = m_run[i];
-      wl[wave][g] = l_run[i];
+  for (int st = 0; st < kSets; ++st)
+#pragma unroll
+    for (int nb = 0; nb < S::kNB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // hi + lo: the lo rows sit 16 lanes (DH 128) or 32 lanes (DH 64) up
+        float v = acc[st][nb][i];
+        v += __shfl_xor(v, DH == 128 ? 16 : 32, kWave);
+        int h;
+        bool keep;
+        float ig, pbv;
+        if constexpr (DH == 128) {
+          const int g = q4 >> 1;
+          h = 4 * st + i;
+          keep = (q4 & 1) == 0 && (n16 >> 3) == g && h < G;
+          const int hc = min(i, (st == 0 ? G : G - 4) - 1);
+          ig = g ? inv1 : inv0;
+          pbv = st == 0 ? (g ? pA1[hc] : pA0[hc]) : (g ? pB1[hc] : pB0[hc]);
+        } else {
+          h = 4 * q4 + i;
+          keep = q4 < 2 && h < G;
+          ig = inv0;
+          if constexpr (G > 4)
+            pbv = (q4 & 1) ? pB0[i] : pA0[i];
+          else
+            pbv = pA0[min(i, G - 1)];
+        }
+        if (keep) wo[wave][h][value_dim<BITS, DH>(n16, nb)] = fmaf(v, ig, pbv);
+      }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      wm[wave][h] = lane_value(mrow[h & 3], 16 * (h / 4));
+      wl[wave][h] = wave < nsteps ? (h < 4 ? lA[h & 3] : lB[h & 3]) : 0.0f;
     }
   }
   __syncthreads();
-  // --- merge the four waves (log-sum-exp) and write the slice partial ---------
+  // --- merge the four waves (log-sum-exp, base 2) and write the slice partial ----
   for (int idx = threadIdx.x; idx < G * DH; idx += kBlock) {
     const int g = idx / DH, dd = idx - g * DH;
     float M = -INFINITY;
@@ -693,7 +919,7 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     float L = 0.0f, O = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float e = wl[w][g] > 0.0f ? expf(wm[w][g] - M) : 0.0f;  // idle waves hold -inf
+      const float e = wl[w][g] > 0.0f ? exp2f(wm[w][g] - M) : 0.0f;  // idle waves hold -inf
       L = fmaf(wl[w][g], e, L);
       O = fmaf(wo[w][g][dd], e, O);
     }
@@ -826,7 +1052,8 @@ extern "C" int kvp_kv_decode(const void* q, const uint32_t* k_wq, const void* k_
   a.chunk = chunk;
   a.n_chunks = n_chunks;
   a.per_seq = cache_per_sequence ? 1 : 0;
-  a.scale = 1.0f / sqrtf((float)head_dim);
+  // Base-2 softmax: scores carry log2(e) / sqrt(DH), rounded once.
+  a.scale = (float)(1.4426950408889634 / sqrt((double)head_dim));
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (bits) {
     case 2: return launch_bits<2>(head_dim, G, a, batch, st);

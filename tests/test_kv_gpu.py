@@ -233,3 +233,73 @@ def test_repeated_steps_reuse_the_workspace():
             first = got
         assert np.array_equal(got, first)
     assert np.isfinite(first).all()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dh", [64, 128])
+@pytest.mark.parametrize("g", [1, 2, 4, 8])
+def test_every_query_group_size(bits, dh, g):
+    """G = H / HKV query heads per KV head, 1 .. 8, on a ragged length (777,
+    not a multiple of the 32-position step), fp32 output."""
+    hkv = 2
+    rng = np.random.default_rng(100 * g + dh + bits)
+    q = rng.standard_normal((1, g * hkv, dh)).astype(np.float16)
+    kc = rng.standard_normal((hkv, 777, dh)).astype(np.float16)
+    vc = rng.standard_normal((hkv, 777, dh)).astype(np.float16)
+    nk = rng.standard_normal((1, hkv, dh)).astype(np.float16)
+    nv = rng.standard_normal((1, hkv, dh)).astype(np.float16)
+    out = run(q, kc, vc, nk, nv, bits, "float32")
+    v = verify_output("kv_attention", kv_gqa_inputs(q, kc, vc, nk, nv, bits), out,
+                      dtype="float32")
+    assert v.ok, (bits, dh, g, v)
+
+
+def ranged_case(rng, g, hkv, t, dh, growth):
+    """V rows scaled by ``growth`` (per position) and K rows that lean on the
+    mean query by -ln(growth), so that p_t * |v_t| stays level along t and
+    every magnitude band matters to the output."""
+    q = rng.standard_normal((1, g * hkv, dh)).astype(np.float16)
+    qbar = q[0].astype(np.float64).reshape(hkv, g, dh).mean(axis=1)
+    beta = -np.log(growth)[None, :] * np.sqrt(dh) / (qbar ** 2).sum(-1, keepdims=True)
+    kc = (beta[..., None] * qbar[:, None, :]
+          + 0.3 * rng.standard_normal((hkv, t, dh))).astype(np.float16)
+    vc = (rng.standard_normal((hkv, t, dh)) * growth[None, :, None]).astype(np.float16)
+    nk = (0.1 * rng.standard_normal((1, hkv, dh))).astype(np.float16)
+    nv = rng.standard_normal((1, hkv, dh)).astype(np.float16)
+    return q, kc, vc, nk, nv
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("profile", ["rising", "falling", "zero_band"])
+@pytest.mark.parametrize("dh,g", [(128, 4), (64, 8)])
+def test_value_scales_across_many_octaves(bits, profile, dh, g):
+    """V scales spanning 2^16 along the cache: the matrix-core value path
+    carries p * s under a per-group power-of-two range shift that must drop
+    when a larger scale arrives (rising), hold precision for small scales
+    after large ones (falling), and survive all-zero groups (zero_band)."""
+    t = 1500
+    rng = np.random.default_rng({"rising": 1, "falling": 2, "zero_band": 3}[profile] + bits)
+    growth = 2.0 ** (np.arange(t) * 16.0 / t - 8.0)
+    if profile == "falling":
+        growth = growth[::-1].copy()
+    q, kc, vc, nk, nv = ranged_case(rng, g, 1, t, dh, growth)
+    if profile == "zero_band":
+        vc[:, t // 3:t // 2] = 0
+    for chunk in (0, 64):
+        out = run(q, kc, vc, nk, nv, bits, "float32", chunk=chunk)
+        v = verify_output("kv_attention", kv_gqa_inputs(q, kc, vc, nk, nv, bits), out,
+                          dtype="float32")
+        assert v.ok, (bits, profile, dh, g, chunk, v)
+
+
+def test_all_zero_values():
+    """V = 0 everywhere in the cache: the output is p_new * new_v / L."""
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((1, 8, 128)).astype(np.float16)
+    kc = rng.standard_normal((2, 600, 128)).astype(np.float16)
+    vc = np.zeros((2, 600, 128), dtype=np.float16)
+    nk = rng.standard_normal((1, 2, 128)).astype(np.float16)
+    nv = rng.standard_normal((1, 2, 128)).astype(np.float16)
+    out = run(q, kc, vc, nk, nv, 4, "float32")
+    v = verify_output("kv_attention", kv_gqa_inputs(q, kc, vc, nk, nv, 4), out, dtype="float32")
+    assert v.ok, v
