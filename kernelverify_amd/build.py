@@ -37,6 +37,9 @@ DEVICE_FLAGS = [
     "-fPIC",
     "-ffp-contract=fast",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in ordinary VGPRs: the KV kernels rescale them
+    # on the VALU, which cannot operate on AGPRs in place
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
     f"-I{INCLUDE}",
 ]

@@ -437,14 +437,16 @@ __device__ __forceinline__ f16x8 codes8_f16(const uint32_t* w) {
 
 // Reductions over the 16 lanes of a DPP row; every lane of the row gets the
 // same (bit-identical) result.
+// (Every source lane of these patterns lies inside the row, so bound_ctrl's
+// zero fill never applies; it spares the old-value initialisation.)
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]
 constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]
@@ -498,51 +500,67 @@ struct KvStepRegs {
   uint32_t vw[8][S::kVW];          // V codes: positions 8 kb + j, the lane's column word
 };
 
+// Buffer resources over one block's slice of the six cache arrays. A read
+// past the slice's last row returns zeros (the hardware range check), so
+// the loads of a partial last step need no clamping: zero K codes and
+// scales give finite scores that the step masks, zero V scales give x = 0.
+struct SliceRsrc {
+  __amdgpu_buffer_rsrc_t kw, ks, kb, vw, vs, vb;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 template <int BITS, int DH>
-__device__ __forceinline__ void load_step(KvStepRegs<BITS, DH>& R, const KvArgs& a, size_t base,
-                                          int p0, int n, int lane) {
+__device__ __forceinline__ void load_step(KvStepRegs<BITS, DH>& R, const SliceRsrc& rs, int p0,
+                                          int lane) {
   using S = KvStepShape<BITS, DH>;
+  constexpr uint32_t kRB = S::kRowWords * 4;  // bytes per cache row
   const int n16 = lane % 16, kb = lane / 16;
+  // Lane byte offsets; the per-step part p0 * row bytes is uniform, the
+  // tile / k-step / position parts are instruction immediates.
+  const uint32_t ko = (uint32_t)(p0 + n16) * kRB + kb * 4 * S::kKW;
+  const uint32_t so = (uint32_t)(p0 + n16) * 2 * S::kGroups;
+  const int col = (BITS == 4 && DH == 64) ? n16 % 8 : n16;
+  const uint32_t vo = (uint32_t)(p0 + 8 * kb) * kRB + col * 4 * S::kVW;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
-    const size_t row = base + min(p0 + kTile * tt + n16, n - 1);
-    const uint32_t* kr = a.k_wq + row * S::kRowWords;
 #pragma unroll
     for (int s = 0; s < S::kKS; ++s) {
+      const uint32_t o = ko + tt * kTile * kRB + s * 16 * S::kKW;
       if constexpr (BITS == 4) {
-        R.kw[tt][s][0] = kr[4 * s + kb];
+        R.kw[tt][s][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.kw, o, 0, 0);
       } else {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(kr + 8 * s + 2 * kb);
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.kw, o, 0, 0);
         R.kw[tt][s][0] = v.x;
         R.kw[tt][s][1] = v.y;
       }
     }
+    const uint32_t o = so + tt * kTile * 2 * S::kGroups;
     if constexpr (S::kGroups == 2) {
-      R.ks[tt] = *reinterpret_cast<const uint32_t*>(a.k_s + row * 2);
-      R.kbias[tt] = *reinterpret_cast<const uint32_t*>(a.k_b + row * 2);
-      R.vs[tt] = *reinterpret_cast<const uint32_t*>(a.v_s + row * 2);
-      R.vbias[tt] = *reinterpret_cast<const uint32_t*>(a.v_b + row * 2);
+      R.ks[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, o, 0, 0);
+      R.kbias[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, o, 0, 0);
+      R.vs[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, o, 0, 0);
+      R.vbias[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, o, 0, 0);
     } else {
-      R.ks[tt] = a.k_s[row];
-      R.kbias[tt] = a.k_b[row];
-      R.vs[tt] = a.v_s[row];
-      R.vbias[tt] = a.v_b[row];
+      R.ks[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, o, 0, 0);
+      R.kbias[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, o, 0, 0);
+      R.vs[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, o, 0, 0);
+      R.vbias[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, o, 0, 0);
     }
   }
   // The lane's column word: 4-bit DH 128 word n16 (dims 8 n16 ..), 8-bit
   // DH 128 words 2 n16, 2 n16 + 1 (dims 8 n16 ..), 4-bit DH 64 word n16 % 8,
   // 8-bit DH 64 word n16 (dims 4 n16 ..).
-  const int col = (BITS == 4 && DH == 64) ? n16 % 8 : n16;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const size_t row = base + min(p0 + 8 * kb + j, n - 1);
-    const uint32_t* vr = a.v_wq + row * S::kRowWords;
     if constexpr (S::kVW == 2) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(vr + 2 * col);
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.vw, vo + j * kRB, 0, 0);
       R.vw[j][0] = v.x;
       R.vw[j][1] = v.y;
     } else {
-      R.vw[j][0] = vr[col];
+      R.vw[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.vw, vo + j * kRB, 0, 0);
     }
   }
 }
@@ -585,10 +603,15 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   constexpr int kHp = G <= 4 ? 4 : 8;             // heads per LDS position row (padded)
   constexpr int kXS = kGroups * kHp;              // floats per position in xbuf
   constexpr int kXWave = kStep * kXS + 4 * 8;     // + 8 floats per 8 positions (bank spread)
+  // Lazy rescale: the max in use may trail the running max by up to 2^kLazy
+  // (p <= 2^kLazy), so accumulators are rescaled only when a head's max
+  // rises further; the range shift leaves room for it (x < 2^15).
+  constexpr float kLazy = 8.0f;
+  constexpr int kEBase = 21;                      // E = kEBase - exponent field of max |s|
   static_assert(G <= 8, "at most 8 query heads per KV head");
   __shared__ __align__(16) float xbuf[kWaves][kXWave];
   __shared__ float wm[kWaves][G], wl[kWaves][G];
-  __shared__ float wo[kWaves][G][DH];
+  __shared__ __align__(16) float wo[kWaves][G][DH];
 
   const int c = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int T = min(max(a.t_cached[b], 0), a.t_stride);
@@ -596,13 +619,24 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   if (slice0 >= T) return;  // block-uniform
   const int n = min(a.chunk, T - slice0);
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int n16 = lane % 16, q4 = lane / 16;
   const int h0 = hk * G;
   const size_t base = ((size_t)(a.per_seq ? b : 0) * a.n_kv_heads + hk) * a.t_stride + slice0;
   const int nsteps = (n + kStep - 1) / kStep;
   float* xw = xbuf[wave];
   auto xaddr = [](int pos, int g, int h) { return pos * kXS + (pos / 8) * 8 + g * kHp + h; };
+
+  SliceRsrc rs;
+  {
+    const uint32_t rb = S::kRowWords * 4, sb = 2 * kGroups;
+    rs.kw = slice_rsrc(a.k_wq + base * S::kRowWords, n * rb);
+    rs.vw = slice_rsrc(a.v_wq + base * S::kRowWords, n * rb);
+    rs.ks = slice_rsrc(a.k_s + base * kGroups, n * sb);
+    rs.kb = slice_rsrc(a.k_b + base * kGroups, n * sb);
+    rs.vs = slice_rsrc(a.v_s + base * kGroups, n * sb);
+    rs.vb = slice_rsrc(a.v_b + base * kGroups, n * sb);
+  }
 
   // Score A operand: query head n16 < G, dims 32 s + 8 q4 + 0..7.
   f16x8 qa[S::kKS];
@@ -618,10 +652,10 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   }
 
   KvStepRegs<BITS, DH> RA, RB;
-  if (wave < nsteps) load_step<BITS, DH>(RA, a, base, kStep * wave, n, lane);
+  if (wave < nsteps) load_step<BITS, DH>(RA, rs, kStep * wave, lane);
 
-  // qsum per group in the score layout (head 4 q4 + i).
-  f32x4 qsum[kGroups];
+  // qsum per group times the softmax scale, in the score layout (head 4 q4 + i).
+  f32x4 qss[kGroups];
   {
     f16x8 ones;
 #pragma unroll
@@ -632,21 +666,18 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
 #pragma unroll
       for (int s = 2 * g; s < 2 * g + 2; ++s)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], ones, acc, 0, 0, 0);
-      qsum[g] = acc;
+      qss[g] = acc * a.scale;
     }
   }
 
-  // Running state. m: per head, wave-uniform (base-2 units). l, pb: per
-  // lane partial sums in the score layout, reduced over the row at the end.
-  // mrow[i]: running max of head 4 q4 + i, the heads of this lane's score
+  // mrow[i]: the max in use for head 4 q4 + i, the heads of this lane's score
   // row (uniform over the row; rows past the last real head hold scores of
-  // zero query rows and are never read).
-  float mrow[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) mrow[i] = -INFINITY;
-  float l[4], pb[4][kGroups];
+  // zero query rows and are never read). l, pb: per lane partial sums in the
+  // score layout, reduced over the row at the end.
+  float mrow[4], l[4], pb[4][kGroups];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    mrow[i] = -INFINITY;
     l[i] = 0.0f;
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) pb[i][g] = 0.0f;
@@ -656,10 +687,8 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   for (int st = 0; st < kSets; ++st)
 #pragma unroll
     for (int nb = 0; nb < S::kNB; ++nb) acc[st][nb] = f32x4{0, 0, 0, 0};
-  int E[kGroups];        // range shift per group (uniform); 127 = no nonzero scale yet
-  uint32_t thr = 0;      // per 16-bit half: largest |V scale| bits that fit the current E
-#pragma unroll
-  for (int g = 0; g < kGroups; ++g) E[g] = 127;
+  int E0 = 127, E1 = 127;  // range shift of groups 0 / 1 (uniform); 127 = no nonzero scale yet
+  uint32_t thr = 0;        // per 16-bit half: largest |V scale| bits the current E admits
 
   const float scale24 = a.scale * 16777216.0f;  // base-2 softmax scale x 2^24 (denormal codes)
   // Value A operand row of this lane: (group, hi/lo part, head).
@@ -683,70 +712,71 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
                                                       0, 0);
         d[g] = a4;
       }
-      const bool valid = p0 + kTile * tt + n16 < n;
+      float sgS[kGroups], bg[kGroups];
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        sgS[g] = f16_bits_to_f32((uint16_t)(R.ks[tt] >> (16 * g))) * scale24;
+        bg[g] = f16_bits_to_f32((uint16_t)(R.kbias[tt] >> (16 * g)));
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = 0.0f;
 #pragma unroll
-        for (int g = 0; g < kGroups; ++g) {
-          const float sg = f16_bits_to_f32((uint16_t)(R.ks[tt] >> (16 * g)));
-          const float bg = f16_bits_to_f32((uint16_t)(R.kbias[tt] >> (16 * g)));
-          v = fmaf(sg * scale24, d[g][i], fmaf(bg * a.scale, qsum[g][i], v));
-        }
-        sv[tt][i] = valid ? v : -INFINITY;
+        for (int g = 0; g < kGroups; ++g) v = fmaf(sgS[g], d[g][i], fmaf(bg[g], qss[g][i], v));
+        sv[tt][i] = v;
       }
     }
-    // --- running max per head (uniform), probabilities --------------------------
-    float mx[4];
+    if (p0 + kStep > n) {  // the slice's partial last step (uniform)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) mx[i] = row16_max(fmaxf(sv[0][i], sv[1][i]));
-    float csel[4];
-    bool grew_lane = false;
+      for (int tt = 0; tt < 2; ++tt) {
+        const bool valid = p0 + kTile * tt + n16 < n;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[tt][i] = valid ? sv[tt][i] : -INFINITY;
+      }
+    }
+    // --- the max in use: moves only when a score outruns it by 2^kLazy ---------
+    uint64_t rise = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float mn = fmaxf(mrow[i], mx[i]);
-      csel[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);
-      grew_lane |= mn > mrow[i];
-      mrow[i] = mn;
+      const float lim = mrow[i] + kLazy;
+      rise |= __builtin_amdgcn_ballot_w64(sv[0][i] > lim) | __builtin_amdgcn_ballot_w64(sv[1][i] > lim);
     }
-    const bool grew = __builtin_amdgcn_ballot_w64(grew_lane) != 0;  // wave-uniform
-    float p[2][4];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - mrow[i]);
-
+    const bool raise = rise != 0;  // wave-uniform
     // --- range shift: a V scale larger than the current E admits -----------------
     const uint32_t ub = __builtin_bit_cast(
-        uint32_t, __builtin_elementwise_max(
-                      __builtin_bit_cast(u16x2, R.vs[0] & 0x7FFF7FFFu),
-                      __builtin_bit_cast(u16x2, R.vs[1] & 0x7FFF7FFFu)));
-    const bool over = __builtin_bit_cast(uint32_t,
-                                         __builtin_elementwise_max(__builtin_bit_cast(u16x2, ub),
-                                                                   __builtin_bit_cast(u16x2, thr))) != thr;
-    float fE0 = 1.0f, fE1 = 1.0f;  // accumulator rescale of groups 0 / 1
-    bool shifted = false;
-    if (__builtin_amdgcn_ballot_w64(over) != 0) {  // wave-uniform, rare
-      uint32_t nthr = 0;
-#pragma unroll
-      for (int g = 0; g < kGroups; ++g) {
-        const int e = __builtin_amdgcn_readlane(row16_max_i((int)((ub >> (16 * g)) & 0xFFFFu)), 0) >> 10;
-        const int en = min(E[g], 29 - e);
-        (g ? fE1 : fE0) = exp2_int(en - E[g]);
-        shifted |= en != E[g];
-        E[g] = en;
-        nthr |= (uint32_t)(((30 - en) << 10) - 1) << (16 * g);
+        uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, R.vs[0] & 0x7FFF7FFFu),
+                                            __builtin_bit_cast(u16x2, R.vs[1] & 0x7FFF7FFFu)));
+    const bool over = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
+                                                       __builtin_bit_cast(u16x2, ub),
+                                                       __builtin_bit_cast(u16x2, thr))) != thr;
+    // One rare, wave-uniform slow path for both: a new max in use and a
+    // lower range shift, each an exact rescale of what has accumulated.
+    if (raise || __builtin_amdgcn_ballot_w64(over) != 0) {
+      const int e0 = __builtin_amdgcn_readlane(row16_max_i((int)(ub & 0xFFFFu)), 0) >> 10;
+      const int n0 = min(E0, kEBase - e0);
+      const float fE0 = exp2_int(n0 - E0);
+      E0 = n0;
+      uint32_t nthr = (uint32_t)(((kEBase + 1 - n0) << 10) - 1);
+      float fE1 = fE0;
+      if constexpr (kGroups == 2) {
+        const int e1 = __builtin_amdgcn_readlane(row16_max_i((int)(ub >> 16)), 0) >> 10;
+        const int n1 = min(E1, kEBase - e1);
+        fE1 = exp2_int(n1 - E1);
+        E1 = n1;
+        nthr |= (uint32_t)(((kEBase + 1 - n1) << 10) - 1) << 16;
       }
       thr = nthr;
-    }
-    if (grew || shifted) {  // wave-uniform
+      float csel[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        // (without a raise, max(mrow, row max) is mrow: csel = 1)
+        const float mn = raise ? fmaxf(mrow[i], row16_max(fmaxf(sv[0][i], sv[1][i]))) : mrow[i];
+        csel[i] = raise ? __builtin_amdgcn_exp2f(mrow[i] - mn) : 1.0f;
+        mrow[i] = mn;
         l[i] *= csel[i];
 #pragma unroll
         for (int g = 0; g < kGroups; ++g) pb[i][g] *= csel[i];
       }
-      // value accumulator rows of this lane: group, head 4 q4 + i (row set st)
 #pragma unroll
       for (int st = 0; st < kSets; ++st) {
         float f[4];
@@ -767,16 +797,19 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
           for (int i = 0; i < 4; ++i) acc[st][nb][i] *= f[i];
       }
     }
-    float sE[kGroups];
+    float p[2][4];
 #pragma unroll
-    for (int g = 0; g < kGroups; ++g) sE[g] = exp2_int(E[g]);
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - mrow[i]);
     // --- l, p * b, and x = p * s * 2^E into LDS (position, group, head) ---------
+    const float sE0 = exp2_int(E0), sE1 = exp2_int(E1);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       float x[kGroups][4];
 #pragma unroll
       for (int g = 0; g < kGroups; ++g) {
-        const float vsg = f16_bits_to_f32((uint16_t)(R.vs[tt] >> (16 * g))) * sE[g];
+        const float vsg = f16_bits_to_f32((uint16_t)(R.vs[tt] >> (16 * g))) * (g ? sE1 : sE0);
         const float vbg = f16_bits_to_f32((uint16_t)(R.vbias[tt] >> (16 * g)));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -793,9 +826,10 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
               f32x4{x[g][0], x[g][1], x[g][2], x[g][3]};
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // The x rows written above are read below by other lanes of this wave: a
+    // wave's LDS operations execute in program order, so keeping the compiler
+    // from moving them across this point is enough.
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // --- values on the matrix cores ---------------------------------------------
     uint32_t pl[8][2];
 #pragma unroll
@@ -845,11 +879,11 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     int t = wave;
     const int last = nsteps - 1;
     for (;;) {
-      load_step<BITS, DH>(RB, a, base, kStep * min(t + kWaves, last), n, lane);
+      load_step<BITS, DH>(RB, rs, kStep * min(t + kWaves, last), lane);
       process(RA, t);
       t += kWaves;
       if (t > last) break;
-      load_step<BITS, DH>(RA, a, base, kStep * min(t + kWaves, last), n, lane);
+      load_step<BITS, DH>(RA, rs, kStep * min(t + kWaves, last), lane);
       process(RB, t);
       t += kWaves;
       if (t > last) break;
@@ -871,37 +905,48 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     pA1[i] = lane_value(p1, 0);
     pB1[i] = lane_value(p1, 16);
   }
-  const float inv0 = exp2_int(24 - E[0]), inv1 = exp2_int(24 - E[kGroups - 1]);
+  const float inv0 = exp2_int(24 - E0), inv1 = exp2_int(24 - E1);
+  // hi + lo: the lo rows sit one 16-lane row up (DH 128) or 32 lanes up
+  // (DH 64). (A plain lane exchange: the two-result lane-swap builtins gave
+  // inconsistent result orders in this compiler.)
+  auto add_lo = [](float v) { return v + __shfl_xor(v, DH == 128 ? 16 : 32, kWave); };
 #pragma unroll
   for (int st = 0; st < kSets; ++st)
 #pragma unroll
-    for (int nb = 0; nb < S::kNB; ++nb)
+    for (int i = 0; i < 4; ++i) {
+      float o[S::kNB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // hi + lo: the lo rows sit 16 lanes (DH 128) or 32 lanes (DH 64) up
-        float v = acc[st][nb][i];
-        v += __shfl_xor(v, DH == 128 ? 16 : 32, kWave);
-        int h;
-        bool keep;
-        float ig, pbv;
-        if constexpr (DH == 128) {
-          const int g = q4 >> 1;
-          h = 4 * st + i;
-          keep = (q4 & 1) == 0 && (n16 >> 3) == g && h < G;
-          const int hc = min(i, (st == 0 ? G : G - 4) - 1);
-          ig = g ? inv1 : inv0;
-          pbv = st == 0 ? (g ? pA1[hc] : pA0[hc]) : (g ? pB1[hc] : pB0[hc]);
-        } else {
-          h = 4 * q4 + i;
-          keep = q4 < 2 && h < G;
-          ig = inv0;
-          if constexpr (G > 4)
-            pbv = (q4 & 1) ? pB0[i] : pA0[i];
-          else
-            pbv = pA0[min(i, G - 1)];
-        }
-        if (keep) wo[wave][h][value_dim<BITS, DH>(n16, nb)] = fmaf(v, ig, pbv);
+      for (int nb = 0; nb < S::kNB; ++nb) o[nb] = add_lo(acc[st][nb][i]);
+      int h, d0;
+      bool keep;
+      float ig, pbv;
+      if constexpr (DH == 128) {
+        // lanes of rows 0 (group 0, dims 0-63) and 2 (group 1, dims 64-127)
+        const int g = q4 >> 1;
+        h = 4 * st + i;
+        keep = (q4 & 1) == 0 && (n16 >> 3) == g && h < G;
+        const int hc = min(i, (st == 0 ? G : G - 4) - 1);
+        ig = g ? inv1 : inv0;
+        pbv = st == 0 ? (g ? pA1[hc] : pA0[hc]) : (g ? pB1[hc] : pB0[hc]);
+        d0 = 8 * n16;
+      } else {
+        h = 4 * q4 + i;
+        keep = q4 < 2 && h < G;
+        ig = inv0;
+        if constexpr (G > 4)
+          pbv = (q4 & 1) ? pB0[i] : pA0[i];
+        else
+          pbv = pA0[min(i, G - 1)];
+        d0 = value_dim<BITS, DH>(n16, 0);
       }
+      if (keep) {
+#pragma unroll
+        for (int v4 = 0; v4 < S::kNB / 4; ++v4)
+          *reinterpret_cast<f32x4*>(&wo[wave][h][d0 + 4 * v4]) =
+              f32x4{fmaf(o[4 * v4], ig, pbv), fmaf(o[4 * v4 + 1], ig, pbv),
+                    fmaf(o[4 * v4 + 2], ig, pbv), fmaf(o[4 * v4 + 3], ig, pbv)};
+      }
+    }
   if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
