@@ -88,12 +88,13 @@ __device__ __forceinline__ uint32_t load_block8(const uint32_t* __restrict__ row
 }
 
 // Merge of the chunk partials of one query head and the new entry:
-// M = max(m_c, s_new), L = sum l_c e^(m_c-M) + e^(s_new-M),
-// out = (sum o_c e^(m_c-M) + e^(s_new-M) new_v) / L.
+// M = max(m_c, s_new), L = sum l_c 2^(m_c-M) + 2^(s_new-M),
+// out = (sum o_c 2^(m_c-M) + 2^(s_new-M) new_v) / L   (base-2 units).
 // One block per (sequence, head, 16-dim slice): the 256 threads are 16
-// chunk groups x 16 dims, so every partial a block needs is requested at
-// once (coalesced 16-float rows) and the merge costs about one memory
-// latency whatever the chunk count.
+// chunk groups x 16 dims. Each thread folds its chunks into a running
+// (M, L, O) as it reads them (one pass, every load issued up front), the
+// sixteen group results meet once in LDS, and the new entry's score is
+// formed by wave 0 while those loads are in flight.
 constexpr int kCombDims = 16;
 constexpr int kCombGroups = kBlock / kCombDims;
 
@@ -106,13 +107,24 @@ __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
   const int T = min(max(a.t_cached[b], 0), a.t_stride);  // as the split kernel clamps it
   const int nc = (T + a.chunk - 1) / a.chunk;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  __shared__ float red[kWaves];
-  __shared__ float s_new_sh, M_sh;
-  __shared__ float osum[kCombGroups][kCombDims];
-  __shared__ float lsum[kCombGroups];
+  __shared__ float s_new_sh;
+  __shared__ float gm[kCombGroups], gl[kCombGroups];
+  __shared__ float go[kCombGroups][kCombDims];
 
   const float* pz = a.part + (size_t)z * a.n_chunks * partial_floats(DH);
-  if (wave == 0) {  // the new entry at full precision: s_new = q . new_k / sqrt(DH)
+  const int dd = threadIdx.x % kCombDims, grp = threadIdx.x / kCombDims;
+  float M = -INFINITY, L = 0.0f, O = 0.0f;
+#pragma unroll 4
+  for (int c = grp; c < nc; c += kCombGroups) {
+    const float* pc = pz + c * partial_floats(DH);
+    const float mc = pc[0], lc = pc[1], oc = pc[2 + d0 + dd];
+    const float mn = fmaxf(M, mc);
+    const float ea = exp2f(M - mn), eb = exp2f(mc - mn);  // first chunk: ea = 2^-inf = 0
+    L = fmaf(L, ea, lc * eb);
+    O = fmaf(O, ea, oc * eb);
+    M = mn;
+  }
+  if (wave == 0) {  // the new entry at full precision: s_new = q . new_k * scale
     const f16* qh = a.q + (size_t)z * DH;
     const f16* nk = a.new_k + ((size_t)b * a.n_kv_heads + hk) * DH;
     float s = 0.0f;
@@ -120,40 +132,28 @@ __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
     s = wave_sum(s) * a.scale;
     if (lane == 0) s_new_sh = s;
   }
-  float m = -INFINITY;
-  for (int c = threadIdx.x; c < nc; c += kBlock) m = fmaxf(m, pz[c * partial_floats(DH)]);
-  m = wave_max(m);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float M = s_new_sh;
-    for (int i = 0; i < kWaves; ++i) M = fmaxf(M, red[i]);
-    M_sh = M;
+  go[grp][dd] = O;
+  if (dd == 0) {
+    gm[grp] = M;
+    gl[grp] = L;
   }
-  __syncthreads();
-  const float M = M_sh;
-  const int dd = threadIdx.x % kCombDims, grp = threadIdx.x / kCombDims;
-  float o = 0.0f, l = 0.0f;
-#pragma unroll 8
-  for (int c = grp; c < nc; c += kCombGroups) {
-    const float* pc = pz + c * partial_floats(DH);
-    const float e = exp2f(pc[0] - M);
-    o = fmaf(pc[2 + d0 + dd], e, o);
-    l = fmaf(pc[1], e, l);
-  }
-  osum[grp][dd] = o;
-  if (dd == 0) lsum[grp] = l;
   __syncthreads();
   if (threadIdx.x < kCombDims) {
-    const float e_new = exp2f(s_new_sh - M);
+    const float s_new = s_new_sh;
+    float Mx = s_new;
+#pragma unroll
+    for (int i = 0; i < kCombGroups; ++i) Mx = fmaxf(Mx, gm[i]);
+    const float e_new = exp2f(s_new - Mx);
     const f16* nv = a.new_v + ((size_t)b * a.n_kv_heads + hk) * DH;
     float v = e_new * (float)nv[d0 + dd];
-    float L = e_new;
+    float Lx = e_new;
+#pragma unroll
     for (int i = 0; i < kCombGroups; ++i) {
-      v += osum[i][dd];
-      L += lsum[i];
+      const float e = gl[i] > 0.0f ? exp2f(gm[i] - Mx) : 0.0f;  // groups without chunks
+      v = fmaf(go[i][dd], e, v);
+      Lx = fmaf(gl[i], e, Lx);
     }
-    store_out<OutT>(static_cast<OutT*>(a.out) + (size_t)z * DH + d0 + dd, v / L);
+    store_out<OutT>(static_cast<OutT*>(a.out) + (size_t)z * DH + d0 + dd, v / Lx);
   }
 }
 
