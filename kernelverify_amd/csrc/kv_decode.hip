@@ -383,19 +383,21 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(KvArgs a) {
 // ---------------------------------------------------------------------------
 // Matrix-core split kernel (4- and 8-bit caches, G <= 8 query heads per KV
 // head): one block per (slice of positions, KV head, sequence). Its four
-// waves work independently on 32-position steps (step t of the slice goes to
-// wave t % 4), each keeping an exact running-max online softmax per head in
-// the base-2 domain, and merge once at the end.
+// waves work independently on steps of 64 positions (32 when G > 4; step t
+// of the slice goes to wave t % 4), each keeping an exact online softmax per
+// head in the base-2 domain, and merge once at the end.
 //
-// Scores, two 16-position tiles per step:
-//   S[h][n] = sum_g s_n,g (Q K_g^T)[h][n] + b_n,g qsum_g[h]
-// over the 64-dim groups g. (Q K_g^T) is a sum of v_mfma_f32_16x16x32_f16:
-// A = the query rows (heads on M, zero past G), B = the codes as exact fp16
-// denormals (c -> c * 2^-24, folded into the score scale), fp32
-// accumulation; qsum_g comes from the same instruction against ones.
+// Scores: S[h][n] = sum_g s_n,g (Q K_g^T)[h][n] + b_n,g qsum_g[h] over the
+// 64-dim groups g, on v_mfma_f32_16x16x32_f16 with the 16 rows of A taken
+// by (position tile, head) pairs: 4 tiles x 4 heads (2 x 8 when G > 4). A's
+// 32-wide k is split the same way, so A carries the query block-diagonally
+// (a slice of a head's row where the tiles match, zeros elsewhere; read from
+// a small LDS table) and B carries each tile's codes as exact fp16
+// denormals (c -> c * 2^-24, folded into the score scale). The output then
+// gives every lane its own position's scores for its heads: no padding
+// rows, and the softmax works on 4 values per lane and step.
 //
-// Values, one v_mfma_f32_16x16x32_f16 per 16 dims over the step's 32
-// positions:
+// Values, one v_mfma_f32_16x16x32_f16 per 16 dims and 32 positions:
 //   O[h][d] = sum_n p[h][n] s_n,g(d) c[n][d] + sum_n p[h][n] b_n,g(d).
 // The first sum runs on the matrix cores: B = the codes (exact fp16
 // denormals), A = x = p * s * 2^E carried as an unevaluated sum of two fp16
@@ -413,8 +415,6 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTile = 16;  // positions per score tile
-constexpr int kStep = 32;  // positions per wave step: two score tiles, one value block
 
 template <int BITS>
 __device__ __forceinline__ f16x8 codes8_f16(const uint32_t* w) {
@@ -479,25 +479,32 @@ __device__ __forceinline__ float exp2_int(int e) {
   return e < -126 ? 0.0f : __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
 }
 
-template <int BITS, int DH>
-struct KvStepShape {
-  static constexpr int kKS = DH / 32;                          // score k-steps per row
-  static constexpr int kKW = BITS == 8 ? 2 : 1;                // words per 8 codes
+template <int BITS, int DH, int G>
+struct KvShape {
+  static constexpr int kGp = G <= 4 ? 4 : 8;        // score rows per tile: heads, padded
+  static constexpr int kTPS = 16 / kGp;             // position tiles per step
+  static constexpr int kP = 16 * kTPS;              // positions per step
+  static constexpr int kHalves = kP / 32;           // 32-position blocks of the value side
+  static constexpr int kSub = 4 / kTPS;             // 8-dim k-blocks per tile and instruction
+  static constexpr int kDPM = 8 * kSub;             // dims of a tile per score instruction
+  static constexpr int kNM = DH / kDPM;             // score instructions per step
   static constexpr int kGroups = DH / 64;
   static constexpr int kRowWords = DH * BITS / 32;
+  static constexpr int kKW = BITS == 8 ? 2 : 1;     // words per 8 codes
+  static constexpr int kKWords = kNM * kKW;         // K words a lane holds per step
   static constexpr int kVW = (BITS == 8 && DH == 128) ? 2 : 1;  // V words per lane and position
-  static constexpr int kNB = DH / 16;                          // value instructions per row set
-  static constexpr int kHR = DH == 128 ? 4 : 8;                // heads per row set
+  static constexpr int kNB = DH / 16;               // value instructions per row set
+  static constexpr int kHR = DH == 128 ? 4 : 8;     // heads per value row set
+  static constexpr int kSets = (G + kHR - 1) / kHR;
 };
 
 // What a lane loads for one step.
-template <int BITS, int DH>
+template <int BITS, int DH, int G>
 struct KvStepRegs {
-  using S = KvStepShape<BITS, DH>;
-  uint32_t kw[2][S::kKS][S::kKW];  // K codes: tile, k-step (lane's position n16, dims 32s+8kb..)
-  uint32_t ks[2], kbias[2];        // K scales / biases at the lane's score position (groups packed)
-  uint32_t vs[2], vbias[2];        // V scales / biases at the lane's score position
-  uint32_t vw[8][S::kVW];          // V codes: positions 8 kb + j, the lane's column word
+  using S = KvShape<BITS, DH, G>;
+  uint32_t kw[S::kKWords];              // K codes of the lane's score position (its k-blocks)
+  uint32_t ks, kbias, vs, vbias;        // scales / biases there (groups packed)
+  uint32_t vw[S::kHalves][8][S::kVW];   // V codes: positions 32 hf + 8 kb + j, column word
 };
 
 // Buffer resources over one block's slice of the six cache arrays. A read
@@ -512,55 +519,67 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const void* p, uint
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int BITS, int DH>
-__device__ __forceinline__ void load_step(KvStepRegs<BITS, DH>& R, const SliceRsrc& rs, int p0,
+template <int BITS, int DH, int G>
+__device__ __forceinline__ void load_step(KvStepRegs<BITS, DH, G>& R, const SliceRsrc& rs, int p0,
                                           int lane) {
-  using S = KvStepShape<BITS, DH>;
+  using S = KvShape<BITS, DH, G>;
   constexpr uint32_t kRB = S::kRowWords * 4;  // bytes per cache row
   const int n16 = lane % 16, kb = lane / 16;
-  // Lane byte offsets; the per-step part p0 * row bytes is uniform, the
-  // tile / k-step / position parts are instruction immediates.
-  const uint32_t ko = (uint32_t)(p0 + n16) * kRB + kb * 4 * S::kKW;
-  const uint32_t so = (uint32_t)(p0 + n16) * 2 * S::kGroups;
-  const int col = (BITS == 4 && DH == 64) ? n16 % 8 : n16;
-  const uint32_t vo = (uint32_t)(p0 + 8 * kb) * kRB + col * 4 * S::kVW;
+  const int sub = kb % S::kSub;
+  // The lane's score position: tile kb / kSub, row n16. Lane byte offsets;
+  // the per-step part p0 * row bytes is uniform, the rest immediates.
+  const uint32_t pos = (uint32_t)(p0 + 16 * (kb / S::kSub) + n16);
+  const uint32_t ko = pos * kRB;
+  if constexpr (S::kSub == 1) {  // the whole row, 16 bytes at a time
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
+    for (int w = 0; w < S::kKWords; w += 4) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs.kw, ko + 4 * w, 0, 0);
+      R.kw[w] = v.x;
+      R.kw[w + 1] = v.y;
+      R.kw[w + 2] = v.z;
+      R.kw[w + 3] = v.w;
+    }
+  } else {  // the lane's 8-dim block of every 16-dim chunk
 #pragma unroll
-    for (int s = 0; s < S::kKS; ++s) {
-      const uint32_t o = ko + tt * kTile * kRB + s * 16 * S::kKW;
-      if constexpr (BITS == 4) {
-        R.kw[tt][s][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.kw, o, 0, 0);
+    for (int s = 0; s < S::kNM; ++s) {
+      const uint32_t o = ko + (uint32_t)((2 * s + sub) * S::kKW * 4);
+      if constexpr (S::kKW == 1) {
+        R.kw[s] = __builtin_amdgcn_raw_buffer_load_b32(rs.kw, o, 0, 0);
       } else {
         const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.kw, o, 0, 0);
-        R.kw[tt][s][0] = v.x;
-        R.kw[tt][s][1] = v.y;
+        R.kw[2 * s] = v.x;
+        R.kw[2 * s + 1] = v.y;
       }
     }
-    const uint32_t o = so + tt * kTile * 2 * S::kGroups;
-    if constexpr (S::kGroups == 2) {
-      R.ks[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, o, 0, 0);
-      R.kbias[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, o, 0, 0);
-      R.vs[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, o, 0, 0);
-      R.vbias[tt] = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, o, 0, 0);
-    } else {
-      R.ks[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, o, 0, 0);
-      R.kbias[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, o, 0, 0);
-      R.vs[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, o, 0, 0);
-      R.vbias[tt] = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, o, 0, 0);
-    }
+  }
+  const uint32_t so = pos * 2 * S::kGroups;
+  if constexpr (S::kGroups == 2) {
+    R.ks = __builtin_amdgcn_raw_buffer_load_b32(rs.ks, so, 0, 0);
+    R.kbias = __builtin_amdgcn_raw_buffer_load_b32(rs.kb, so, 0, 0);
+    R.vs = __builtin_amdgcn_raw_buffer_load_b32(rs.vs, so, 0, 0);
+    R.vbias = __builtin_amdgcn_raw_buffer_load_b32(rs.vb, so, 0, 0);
+  } else {
+    R.ks = __builtin_amdgcn_raw_buffer_load_b16(rs.ks, so, 0, 0);
+    R.kbias = __builtin_amdgcn_raw_buffer_load_b16(rs.kb, so, 0, 0);
+    R.vs = __builtin_amdgcn_raw_buffer_load_b16(rs.vs, so, 0, 0);
+    R.vbias = __builtin_amdgcn_raw_buffer_load_b16(rs.vb, so, 0, 0);
   }
   // The lane's column word: 4-bit DH 128 word n16 (dims 8 n16 ..), 8-bit
   // DH 128 words 2 n16, 2 n16 + 1 (dims 8 n16 ..), 4-bit DH 64 word n16 % 8,
   // 8-bit DH 64 word n16 (dims 4 n16 ..).
+  const int col = (BITS == 4 && DH == 64) ? n16 % 8 : n16;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if constexpr (S::kVW == 2) {
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.vw, vo + j * kRB, 0, 0);
-      R.vw[j][0] = v.x;
-      R.vw[j][1] = v.y;
-    } else {
-      R.vw[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.vw, vo + j * kRB, 0, 0);
+  for (int hf = 0; hf < S::kHalves; ++hf) {
+    const uint32_t vo = (uint32_t)(p0 + 32 * hf + 8 * kb) * kRB + col * 4 * S::kVW;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (S::kVW == 2) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs.vw, vo + j * kRB, 0, 0);
+        R.vw[hf][j][0] = v.x;
+        R.vw[hf][j][1] = v.y;
+      } else {
+        R.vw[hf][j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs.vw, vo + j * kRB, 0, 0);
+      }
     }
   }
 }
@@ -594,21 +613,28 @@ __device__ __forceinline__ f16x8 value_codes(const uint32_t (&pl)[8][2]) {
   return __builtin_bit_cast(f16x8, u32x4{h[0], h[1], h[2], h[3]});
 }
 
+// Wave-wide max of an int / float (every lane gets it).
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = row16_max_i(v);
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 template <int BITS, int DH, int G>
 __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
-  using S = KvStepShape<BITS, DH>;
-  constexpr int kGroups = S::kGroups;
-  constexpr int kHR = S::kHR;
-  constexpr int kSets = (G + kHR - 1) / kHR;      // value row sets
-  constexpr int kHp = G <= 4 ? 4 : 8;             // heads per LDS position row (padded)
+  using S = KvShape<BITS, DH, G>;
+  constexpr int kGroups = S::kGroups, kGp = S::kGp, kP = S::kP, kHR = S::kHR, kSets = S::kSets;
+  constexpr int kHp = kGp;                        // heads per LDS x row
   constexpr int kXS = kGroups * kHp;              // floats per position in xbuf
-  constexpr int kXWave = kStep * kXS + 4 * 8;     // + 8 floats per 8 positions (bank spread)
+  constexpr int kXWave = kP * kXS + (kP / 8) * 8; // + 8 floats per 8 positions (bank spread)
   // Lazy rescale: the max in use may trail the running max by up to 2^kLazy
-  // (p <= 2^kLazy), so accumulators are rescaled only when a head's max
-  // rises further; the range shift leaves room for it (x < 2^15).
+  // (p <= 2^kLazy), so accumulators are rescaled only when a score rises
+  // further; the range shift leaves room for it (x < 2^15).
   constexpr float kLazy = 8.0f;
   constexpr int kEBase = 21;                      // E = kEBase - exponent field of max |s|
   static_assert(G <= 8, "at most 8 query heads per KV head");
+  __shared__ __align__(16) _Float16 qtab[(G + 1) * DH];  // the G query rows, then zeros
+  __shared__ float qss_sh[G][kGroups];
   __shared__ __align__(16) float xbuf[kWaves][kXWave];
   __shared__ float wm[kWaves][G], wl[kWaves][G];
   __shared__ __align__(16) float wo[kWaves][G][DH];
@@ -623,7 +649,7 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   const int n16 = lane % 16, q4 = lane / 16;
   const int h0 = hk * G;
   const size_t base = ((size_t)(a.per_seq ? b : 0) * a.n_kv_heads + hk) * a.t_stride + slice0;
-  const int nsteps = (n + kStep - 1) / kStep;
+  const int nsteps = (n + kP - 1) / kP;
   float* xw = xbuf[wave];
   auto xaddr = [](int pos, int g, int h) { return pos * kXS + (pos / 8) * 8 + g * kHp + h; };
 
@@ -637,43 +663,46 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     rs.vs = slice_rsrc(a.v_s + base * kGroups, n * sb);
     rs.vb = slice_rsrc(a.v_b + base * kGroups, n * sb);
   }
+  KvStepRegs<BITS, DH, G> RA, RB;
+  if (wave < nsteps) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
 
-  // Score A operand: query head n16 < G, dims 32 s + 8 q4 + 0..7.
-  f16x8 qa[S::kKS];
-#pragma unroll
-  for (int s = 0; s < S::kKS; ++s) {
-    if (n16 < G) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + n16) * DH +
-                                                       32 * s + 8 * q4);
-      qa[s] = __builtin_bit_cast(f16x8, v);
-    } else {
-      qa[s] = f16x8{};
-    }
+  // Query table in LDS (G rows, then a zero row), and qsum_g[h] * scale.
+  for (int i = threadIdx.x; i < (G + 1) * (DH / 8); i += kBlock) {
+    const int row = i / (DH / 8), c8 = i % (DH / 8);
+    u32x4 v = {0, 0, 0, 0};
+    if (row < G)
+      v = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + row) * DH + 8 * c8);
+    *reinterpret_cast<u32x4*>(&qtab[row * DH + 8 * c8]) = v;
   }
-
-  KvStepRegs<BITS, DH> RA, RB;
-  if (wave < nsteps) load_step<BITS, DH>(RA, rs, kStep * wave, lane);
-
-  // qsum per group times the softmax scale, in the score layout (head 4 q4 + i).
-  f32x4 qss[kGroups];
+  __syncthreads();
   {
-    f16x8 ones;
+    const int item = threadIdx.x / 16, part = threadIdx.x % 16;  // 16 lanes per (head, group)
+    float sq = 0.0f;
+    if (item < G * kGroups) {
+      const int hh = item / kGroups, g = item % kGroups;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ones[i] = (_Float16)1.0f;
-#pragma unroll
-    for (int g = 0; g < kGroups; ++g) {
-      f32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-      for (int s = 2 * g; s < 2 * g + 2; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], ones, acc, 0, 0, 0);
-      qss[g] = acc * a.scale;
+      for (int k = 0; k < 4; ++k) sq += (float)qtab[hh * DH + 64 * g + 4 * part + k];
     }
+    sq = row16_sum(sq);
+    if (item < G * kGroups && part == 0) qss_sh[item / kGroups][item % kGroups] = sq * a.scale;
   }
+  __syncthreads();
 
-  // mrow[i]: the max in use for head 4 q4 + i, the heads of this lane's score
-  // row (uniform over the row; rows past the last real head hold scores of
-  // zero query rows and are never read). l, pb: per lane partial sums in the
-  // score layout, reduced over the row at the end.
+  // Score layout: lane holds position 16 (q4 / kSub) + n16 of the step for
+  // heads hd(i) = (kGp == 4 ? i : 4 (q4 % 2) + i), i = 0..3.
+  const int spos = 16 * (q4 / S::kSub) + n16;
+  const int hbase = kGp == 4 ? 0 : 4 * (q4 % 2);
+  float qss[kGroups][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) qss[g][i] = qss_sh[min(hbase + i, G - 1)][g];
+  // Score A operand: row m = n16 is (tile m / kGp, head m % kGp), k-block q4
+  // is (tile q4 / kSub, dims 8 (q4 % kSub) ..): the query slice on the
+  // block diagonal, zeros elsewhere (the zero row of the table).
+  const int qrow = (n16 / kGp == q4 / S::kSub && n16 % kGp < G) ? n16 % kGp : G;
+  const _Float16* qa = &qtab[qrow * DH + 8 * (q4 % S::kSub)];
+
   float mrow[4], l[4], pb[4][kGroups];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -696,70 +725,63 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   const int hl_r = DH == 128 ? (n16 & 3) : (n16 & 7);
   const float lo_r = (DH == 128 ? (n16 >> 2) & 1 : n16 >> 3) ? 1.0f : 0.0f;
 
-  auto process = [&](const KvStepRegs<BITS, DH>& R, int t) {
-    const int p0 = kStep * t;
-    // --- scores of the two tiles ---------------------------------------------
-    float sv[2][4];
+  auto process = [&](const KvStepRegs<BITS, DH, G>& R, int t) {
+    const int p0 = kP * t;
+    // --- scores: kTPS tiles stacked on the rows of each instruction -----------
+    f32x4 d[kGroups];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      f32x4 d[kGroups];
+    for (int g = 0; g < kGroups; ++g) d[g] = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int g = 0; g < kGroups; ++g) {
-        f32x4 a4 = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 2 * g; s < 2 * g + 2; ++s)
-          a4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], codes8_f16<BITS>(R.kw[tt][s]), a4, 0,
-                                                      0, 0);
-        d[g] = a4;
-      }
+    for (int s = 0; s < S::kNM; ++s) {
+      const f16x8 av = *reinterpret_cast<const f16x8*>(qa + S::kDPM * s);
+      constexpr int kPerGroup = 64 / S::kDPM;
+      d[s / kPerGroup] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          av, codes8_f16<BITS>(&R.kw[s * S::kKW]), d[s / kPerGroup], 0, 0, 0);
+    }
+    float sv[4];
+    {
       float sgS[kGroups], bg[kGroups];
 #pragma unroll
       for (int g = 0; g < kGroups; ++g) {
-        sgS[g] = f16_bits_to_f32((uint16_t)(R.ks[tt] >> (16 * g))) * scale24;
-        bg[g] = f16_bits_to_f32((uint16_t)(R.kbias[tt] >> (16 * g)));
+        sgS[g] = f16_bits_to_f32((uint16_t)(R.ks >> (16 * g))) * scale24;
+        bg[g] = f16_bits_to_f32((uint16_t)(R.kbias >> (16 * g)));
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = 0.0f;
 #pragma unroll
         for (int g = 0; g < kGroups; ++g) v = fmaf(sgS[g], d[g][i], fmaf(bg[g], qss[g][i], v));
-        sv[tt][i] = v;
+        sv[i] = v;
       }
     }
-    if (p0 + kStep > n) {  // the slice's partial last step (uniform)
+    if (p0 + kP > n) {  // the slice's partial last step (uniform)
+      const bool valid = p0 + spos < n;
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const bool valid = p0 + kTile * tt + n16 < n;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[tt][i] = valid ? sv[tt][i] : -INFINITY;
-      }
+      for (int i = 0; i < 4; ++i) sv[i] = valid ? sv[i] : -INFINITY;
     }
     // --- the max in use: moves only when a score outruns it by 2^kLazy ---------
     uint64_t rise = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lim = mrow[i] + kLazy;
-      rise |= __builtin_amdgcn_ballot_w64(sv[0][i] > lim) | __builtin_amdgcn_ballot_w64(sv[1][i] > lim);
-    }
+    for (int i = 0; i < 4; ++i)
+      if (kGp == 8 || i < G)  // heads past G (zero query rows) never move the max
+        rise |= __builtin_amdgcn_ballot_w64(sv[i] > mrow[i] + kLazy);
     const bool raise = rise != 0;  // wave-uniform
     // --- range shift: a V scale larger than the current E admits -----------------
-    const uint32_t ub = __builtin_bit_cast(
-        uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, R.vs[0] & 0x7FFF7FFFu),
-                                            __builtin_bit_cast(u16x2, R.vs[1] & 0x7FFF7FFFu)));
+    const uint32_t ub = R.vs & 0x7FFF7FFFu;
     const bool over = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
                                                        __builtin_bit_cast(u16x2, ub),
                                                        __builtin_bit_cast(u16x2, thr))) != thr;
     // One rare, wave-uniform slow path for both: a new max in use and a
     // lower range shift, each an exact rescale of what has accumulated.
     if (raise || __builtin_amdgcn_ballot_w64(over) != 0) {
-      const int e0 = __builtin_amdgcn_readlane(row16_max_i((int)(ub & 0xFFFFu)), 0) >> 10;
+      const int e0 = wave_max_i((int)(ub & 0xFFFFu)) >> 10;
       const int n0 = min(E0, kEBase - e0);
       const float fE0 = exp2_int(n0 - E0);
       E0 = n0;
       uint32_t nthr = (uint32_t)(((kEBase + 1 - n0) << 10) - 1);
       float fE1 = fE0;
       if constexpr (kGroups == 2) {
-        const int e1 = __builtin_amdgcn_readlane(row16_max_i((int)(ub >> 16)), 0) >> 10;
+        const int e1 = wave_max_i((int)(ub >> 16)) >> 10;
         const int n1 = min(E1, kEBase - e1);
         fE1 = exp2_int(n1 - E1);
         E1 = n1;
@@ -769,9 +791,17 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
       float csel[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        // (without a raise, max(mrow, row max) is mrow: csel = 1)
-        const float mn = raise ? fmaxf(mrow[i], row16_max(fmaxf(sv[0][i], sv[1][i]))) : mrow[i];
-        csel[i] = raise ? __builtin_amdgcn_exp2f(mrow[i] - mn) : 1.0f;
+        float mn = mrow[i];
+        if (raise) {
+          // max over the lanes holding head hd(i): the whole wave (kGp 4) or
+          // score rows q4 and q4 ^ 2 (kGp 8)
+          const float r = row16_max(sv[i]);
+          const float rA = fmaxf(lane_value(r, 0), lane_value(r, 32));
+          const float rB = fmaxf(lane_value(r, 16), lane_value(r, 48));
+          const float hm = kGp == 4 ? fmaxf(rA, rB) : ((q4 & 1) ? rB : rA);
+          mn = fmaxf(mrow[i], hm);
+        }
+        csel[i] = __builtin_amdgcn_exp2f(mrow[i] - mn);  // 1 without a raise
         mrow[i] = mn;
         l[i] *= csel[i];
 #pragma unroll
@@ -782,14 +812,11 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
         float f[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if constexpr (DH == 128) {
-            // row set st holds heads 4 st + i (score row st); the lane's group is q4 / 2
-            f[i] = lane_value(csel[i], 16 * st) * ((q4 >> 1) ? fE1 : fE0);
-          } else {
-            // heads 4 (q4 % 2) + i (score row q4 % 2)
-            const float c0 = lane_value(csel[i], 0), c1 = lane_value(csel[i], 16);
-            f[i] = ((q4 & 1) ? c1 : c0) * fE0;
-          }
+          // value rows of this lane: head kHR st + i (DH 128) or 4 (q4 % 2) + i
+          // (DH 64); their factor sits in score row st (kGp 8, DH 128) or in
+          // this lane's own score row
+          const float ch = (kGp == 8 && DH == 128) ? lane_value(csel[i], 16 * st) : csel[i];
+          f[i] = ch * ((DH == 128 && (q4 >> 1)) ? fE1 : fE0);
         }
 #pragma unroll
         for (int nb = 0; nb < S::kNB; ++nb)
@@ -797,76 +824,71 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
           for (int i = 0; i < 4; ++i) acc[st][nb][i] *= f[i];
       }
     }
-    float p[2][4];
+    // --- p, l, p * b, and x = p * s * 2^E into LDS (position, group, head) ------
+    float p[4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) p[tt][i] = __builtin_amdgcn_exp2f(sv[tt][i] - mrow[i]);
-    // --- l, p * b, and x = p * s * 2^E into LDS (position, group, head) ---------
+    for (int i = 0; i < 4; ++i) {
+      p[i] = __builtin_amdgcn_exp2f(sv[i] - mrow[i]);
+      l[i] += p[i];
+    }
     const float sE0 = exp2_int(E0), sE1 = exp2_int(E1);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      float x[kGroups][4];
+    for (int g = 0; g < kGroups; ++g) {
+      const float vsg = f16_bits_to_f32((uint16_t)(R.vs >> (16 * g))) * (g ? sE1 : sE0);
+      const float vbg = f16_bits_to_f32((uint16_t)(R.vbias >> (16 * g)));
+      f32x4 x;
 #pragma unroll
-      for (int g = 0; g < kGroups; ++g) {
-        const float vsg = f16_bits_to_f32((uint16_t)(R.vs[tt] >> (16 * g))) * (g ? sE1 : sE0);
-        const float vbg = f16_bits_to_f32((uint16_t)(R.vbias[tt] >> (16 * g)));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[g][i] = p[tt][i] * vsg;
-          pb[i][g] = fmaf(p[tt][i], vbg, pb[i][g]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        x[i] = p[i] * vsg;
+        pb[i][g] = fmaf(p[i], vbg, pb[i][g]);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) l[i] += p[tt][i];
-      if (q4 < (G + 3) / 4) {
-#pragma unroll
-        for (int g = 0; g < kGroups; ++g)
-          *reinterpret_cast<f32x4*>(&xw[xaddr(kTile * tt + n16, g, 4 * q4)]) =
-              f32x4{x[g][0], x[g][1], x[g][2], x[g][3]};
-      }
+      *reinterpret_cast<f32x4*>(&xw[xaddr(spos, g, hbase)]) = x;
     }
     // The x rows written above are read below by other lanes of this wave: a
     // wave's LDS operations execute in program order, so keeping the compiler
     // from moving them across this point is enough.
     __builtin_amdgcn_wave_barrier();
-    // --- values on the matrix cores ---------------------------------------------
-    uint32_t pl[8][2];
+    // --- values on the matrix cores, 32 positions per instruction --------------
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if constexpr (BITS == 4) {
-        const uint32_t w = DH == 64 ? (n16 >= 8 ? R.vw[j][0] >> 16 : R.vw[j][0]) : R.vw[j][0];
-        pl[j][0] = w & 0x0F0F0F0Fu;
-        pl[j][1] = (w >> 4) & 0x0F0F0F0Fu;
-      } else {
-        pl[j][0] = R.vw[j][0];
-        pl[j][1] = S::kVW == 2 ? R.vw[j][S::kVW - 1] : 0u;
-      }
-    }
-#pragma unroll
-    for (int st = 0; st < kSets; ++st) {
-      const int h = min(kHR * st + hl_r, G - 1);  // rows past G repeat a real head
-      f16x8 av;
+    for (int hf = 0; hf < S::kHalves; ++hf) {
+      uint32_t pl[8][2];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float xv = xw[xaddr(8 * q4 + j, g_r, h)];
-        const _Float16 hi = (_Float16)xv;
-        av[j] = (_Float16)fmaf(-lo_r, (float)hi, xv);
+        if constexpr (BITS == 4) {
+          const uint32_t w = DH == 64 ? (n16 >= 8 ? R.vw[hf][j][0] >> 16 : R.vw[hf][j][0])
+                                      : R.vw[hf][j][0];
+          pl[j][0] = w & 0x0F0F0F0Fu;
+          pl[j][1] = (w >> 4) & 0x0F0F0F0Fu;
+        } else {
+          pl[j][0] = R.vw[hf][j][0];
+          pl[j][1] = S::kVW == 2 ? R.vw[hf][j][S::kVW - 1] : 0u;
+        }
       }
-      auto mm = [&](auto nbc) {
-        constexpr int NB = decltype(nbc)::value;
-        acc[st][NB] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, value_codes<BITS, DH, NB>(pl),
-                                                            acc[st][NB], 0, 0, 0);
-      };
-      mm(std::integral_constant<int, 0>{});
-      mm(std::integral_constant<int, 1>{});
-      mm(std::integral_constant<int, 2>{});
-      mm(std::integral_constant<int, 3>{});
-      if constexpr (S::kNB == 8) {
-        mm(std::integral_constant<int, 4>{});
-        mm(std::integral_constant<int, 5>{});
-        mm(std::integral_constant<int, 6>{});
-        mm(std::integral_constant<int, 7>{});
+#pragma unroll
+      for (int st = 0; st < kSets; ++st) {
+        const int h = min(kHR * st + hl_r, G - 1);  // rows past G repeat a real head
+        f16x8 av;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xv = xw[xaddr(32 * hf + 8 * q4 + j, g_r, h)];
+          const _Float16 hi = (_Float16)xv;
+          av[j] = (_Float16)fmaf(-lo_r, (float)hi, xv);
+        }
+        auto mm = [&](auto nbc) {
+          constexpr int NB = decltype(nbc)::value;
+          acc[st][NB] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, value_codes<BITS, DH, NB>(pl),
+                                                              acc[st][NB], 0, 0, 0);
+        };
+        mm(std::integral_constant<int, 0>{});
+        mm(std::integral_constant<int, 1>{});
+        mm(std::integral_constant<int, 2>{});
+        mm(std::integral_constant<int, 3>{});
+        if constexpr (S::kNB == 8) {
+          mm(std::integral_constant<int, 4>{});
+          mm(std::integral_constant<int, 5>{});
+          mm(std::integral_constant<int, 6>{});
+          mm(std::integral_constant<int, 7>{});
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();  // xbuf is rewritten by the next step
@@ -879,11 +901,11 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     int t = wave;
     const int last = nsteps - 1;
     for (;;) {
-      load_step<BITS, DH>(RB, rs, kStep * min(t + kWaves, last), lane);
+      load_step<BITS, DH, G>(RB, rs, kP * min(t + kWaves, last), lane);
       process(RA, t);
       t += kWaves;
       if (t > last) break;
-      load_step<BITS, DH>(RA, rs, kStep * min(t + kWaves, last), lane);
+      load_step<BITS, DH, G>(RA, rs, kP * min(t + kWaves, last), lane);
       process(RB, t);
       t += kWaves;
       if (t > last) break;
@@ -891,19 +913,30 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   }
 
   // --- wave results ---------------------------------------------------------------
-  // Row sums of l and p * b, uniform per head: heads 0-3 from row 0, 4-7 from row 1.
+  // Sums of l and p * b over the lanes holding each head: heads 0-3 in score
+  // rows 0 and 2, 4-7 in rows 1 and 3 (kGp 8), all four rows for kGp 4.
   f32x4 lA, lB, pA0, pA1, pB0, pB1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float ls = row16_sum(l[i]);
-    const float p0 = row16_sum(pb[i][0]);
-    const float p1 = row16_sum(pb[i][kGroups - 1]);
-    lA[i] = lane_value(ls, 0);
-    lB[i] = lane_value(ls, 16);
-    pA0[i] = lane_value(p0, 0);
-    pB0[i] = lane_value(p0, 16);
-    pA1[i] = lane_value(p1, 0);
-    pB1[i] = lane_value(p1, 16);
+    const float p0s = row16_sum(pb[i][0]);
+    const float p1s = row16_sum(pb[i][kGroups - 1]);
+    auto rows = [](float v, int r0, int r1) { return lane_value(v, 16 * r0) + lane_value(v, 16 * r1); };
+    if constexpr (kGp == 4) {
+      lA[i] = rows(ls, 0, 2) + rows(ls, 1, 3);
+      pA0[i] = rows(p0s, 0, 2) + rows(p0s, 1, 3);
+      pA1[i] = rows(p1s, 0, 2) + rows(p1s, 1, 3);
+      lB[i] = lA[i];
+      pB0[i] = pA0[i];
+      pB1[i] = pA1[i];
+    } else {
+      lA[i] = rows(ls, 0, 2);
+      lB[i] = rows(ls, 1, 3);
+      pA0[i] = rows(p0s, 0, 2);
+      pB0[i] = rows(p0s, 1, 3);
+      pA1[i] = rows(p1s, 0, 2);
+      pB1[i] = rows(p1s, 1, 3);
+    }
   }
   const float inv0 = exp2_int(24 - E0), inv1 = exp2_int(24 - E1);
   // hi + lo: the lo rows sit one 16-lane row up (DH 128) or 32 lanes up
