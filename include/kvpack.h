@@ -107,13 +107,14 @@ int kvp_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* 
  *   new_k, new_v fp16   [batch][n_kv_heads][head_dim]  (this step's entry,
  *                        used at full precision as position t_cached[b])
  *   t_cached     int32  [batch] device array: cached positions of each
- *                        sequence, 0 <= t_cached[b] <= t_stride
+ *                        sequence (read as min(max(t_cached[b], 0), t_stride))
  *   out          fp16 or fp32 [batch][n_heads][head_dim]
  * Query head h reads cache head h / (n_heads / n_kv_heads) (GQA, :99-103).
  * Scores are scaled by 1/sqrt(head_dim). head_dim in {64, 128};
  * bits in {2, 3, 4, 8}; n_heads % n_kv_heads == 0.
  * chunk: cached positions per split (0 = the library's choice); a multiple
- * of 64. workspace: at least kvp_kv_decode_workspace_bytes(...) bytes.
+ * of 64. workspace: at least kvp_kv_decode_workspace_bytes(...) bytes;
+ * calls sharing a workspace must be ordered (one stream).
  * ---------------------------------------------------------------------- */
 size_t kvp_kv_decode_workspace_bytes(int batch, int n_heads, int head_dim, int t_stride,
                                      int chunk);
