@@ -1012,12 +1012,15 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
 
 bool use_mfma(int bits, int G) { return (bits == 4 || bits == 8) && G <= 8; }
 
-int pick_chunk(int bits, int batch, int n_kv_heads, int t_stride) {
-  // About 1024 blocks over the longest sequence, whole 64-position steps,
-  // at most the kernel's own bound (register-prefetched chunk: 128; the
-  // matrix-core kernel walks its slice tile by tile: 1024).
-  const int cap = (bits == 4 || bits == 8) ? 1024 : 128;
-  long target = (long)batch * n_kv_heads * t_stride / 1024;
+int pick_chunk(int bits, int batch, int n_kv_heads, int t_stride, int G) {
+  // Whole 64-position steps, at most the kernel's own bound. The matrix-core
+  // kernel walks its slice step by step with four waves that each pay a
+  // fixed set-up and merge: about one block per CU (256 over the longest
+  // sequence) measured best. The register-prefetched kernel holds its whole
+  // chunk (128 positions at most): about 1024 blocks.
+  const bool mfma = use_mfma(bits, G);
+  const int cap = mfma ? 1024 : 128;
+  const long target = (long)batch * n_kv_heads * t_stride / (mfma ? 256 : 1024);
   int chunk = 64;
   while (chunk < cap && chunk < target) chunk *= 2;
   return chunk;
@@ -1099,7 +1102,7 @@ extern "C" int kvp_kv_decode(const void* q, const uint32_t* k_wq, const void* k_
   const int G = n_heads / n_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return set_error(KVP_UNSUPPORTED, "kvp_kv_decode: GQA ratio %d not in {1,2,4,8}", G);
-  if (chunk <= 0) chunk = pick_chunk(bits, batch, n_kv_heads, t_stride);
+  if (chunk <= 0) chunk = pick_chunk(bits, batch, n_kv_heads, t_stride, G);
   KVP_REQUIRE(chunk % 64 == 0 && chunk >= 64, "kvp_kv_decode: chunk=%d (a multiple of 64)",
               chunk);
   const int n_chunks = t_stride > 0 ? (t_stride + chunk - 1) / chunk : 1;

@@ -55,9 +55,10 @@ def max_chunk(bits: int, gqa: int = 4) -> int:
 def launch_config(batch: int, n_kv_heads: int, t_stride: int, bits: int = 4,
                   chunk: int | None = None, gqa: int = 4):
     """(grid, block, chunk): one block per (chunk, KV head, sequence); the
-    library's own chunk choice (about 1024 blocks) when ``chunk`` is None."""
+    library's own chunk choice when ``chunk`` is None: about 256 blocks for
+    the matrix-core kernel, about 1024 for the register-prefetched one."""
     if not chunk:
-        target = batch * n_kv_heads * t_stride // 1024
+        target = batch * n_kv_heads * t_stride // (256 if uses_matrix_cores(bits, gqa) else 1024)
         chunk = 64
         while chunk < max_chunk(bits, gqa) and chunk < target:
             chunk *= 2
