@@ -24,7 +24,14 @@ int set_error(int status, const char* fmt, ...) {
   return status;
 }
 
-void clear_error() { g_last_error.clear(); }
+// Entry points start here: the message is reset, and so is the runtime's
+// per-thread last error, which an earlier unrelated HIP call on this thread
+// (a failed symbol lookup, say) may have left behind for check_launch to
+// misreport as this entry's launch failure.
+void clear_error() {
+  g_last_error.clear();
+  (void)hipGetLastError();
+}
 
 int check_launch(const char* what) {
   hipError_t err = hipGetLastError();

@@ -65,6 +65,13 @@ def runtime() -> ctypes.CDLL:
         "hipGraphLaunch": [vp, vp],
         "hipGraphExecDestroy": [vp],
         "hipGraphDestroy": [vp],
+        # module API: run-time compiled kernels (kernelverify_amd/runners/rtc.py)
+        "hipModuleLoadData": [ctypes.POINTER(vp), vp],
+        "hipModuleGetFunction": [ctypes.POINTER(vp), vp, ctypes.c_char_p],
+        "hipModuleLaunchKernel": [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                                  ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp,
+                                  ctypes.POINTER(vp), ctypes.POINTER(vp)],
+        "hipModuleUnload": [vp],
     }
     for name, args in sigs.items():
         fn = getattr(lib, name)
@@ -77,7 +84,9 @@ def runtime() -> ctypes.CDLL:
 
 def check(err: int, what: str) -> None:
     if err != 0:
-        msg = runtime().hipGetErrorString(err).decode(errors="replace")
+        rt = runtime()
+        rt.hipGetLastError()  # consumed here, so no later launch check reports it
+        msg = rt.hipGetErrorString(err).decode(errors="replace")
         raise HipError(f"{what}: {msg} (hipError {err})")
 
 

@@ -163,3 +163,38 @@ def kv_decode(q, k_wq, k_s, k_b, v_wq, v_s, v_b, new_k, new_v, t_cached, *, bits
     KvDecodeCall(*dev, out, bits=bits, cache_per_sequence=cache_per_sequence, chunk=chunk)()
     hip.synchronize()
     return out.to_host()
+
+
+def kernel_spec():
+    """The runner-door template (reference: kernelverify/pack/kv_attention.py:292-352).
+
+    A pack-library descriptor: `specialize()` fills `T`, `BITS` and `DH`;
+    the bindings keep the reference's names and order (q, k_wq .. v_biases,
+    new_k, new_v, out, then the scalars n_heads, t_cached, n_kv_heads,
+    t_stride). The caches are the reference's shared (HKV, T_stride, ...)
+    layout; `t_cached` is the logical length of every batch row, with no
+    capacity bound. The grid's ``b_rows x n_heads`` extent is informational.
+    """
+    from kernelverify_amd.runners import Binding, BindingKind, KernelSpec, LaunchMode, LaunchSpec
+
+    return KernelSpec(
+        source="kvpack:kv_attention T=$T BITS=$BITS DH=$DH",
+        entry_point=KERNEL_NAME,
+        name=f"{KERNEL_NAME}-$BITS bit-DH$DH-$T",
+        bindings=(Binding(BindingKind.INPUT, "q"),
+                  Binding(BindingKind.INPUT, "k_wq"),
+                  Binding(BindingKind.INPUT, "k_scales"),
+                  Binding(BindingKind.INPUT, "k_biases"),
+                  Binding(BindingKind.INPUT, "v_wq"),
+                  Binding(BindingKind.INPUT, "v_scales"),
+                  Binding(BindingKind.INPUT, "v_biases"),
+                  Binding(BindingKind.INPUT, "new_k"),
+                  Binding(BindingKind.INPUT, "new_v"),
+                  Binding(BindingKind.OUTPUT),
+                  Binding(BindingKind.SCALAR, "n_heads", "uint32"),
+                  Binding(BindingKind.SCALAR, "t_cached", "uint32"),
+                  Binding(BindingKind.SCALAR, "n_kv_heads", "uint32"),
+                  Binding(BindingKind.SCALAR, "t_stride", "uint32")),
+        launch=LaunchSpec(grid=(1, 1, ["b_rows", "n_heads"]), threadgroup=(256, 1, 1),
+                          mode=LaunchMode.THREADGROUPS),
+    )

@@ -188,3 +188,67 @@ def swiglu_host(x, idx, gate, gate_w, up_w, down_w, *, bits: int, out_dtype: str
     out = DeviceArray((x.shape[0], x.shape[1]), out_dtype)
     SwigluCall(dx, di, dg, up(gate_w), up(up_w), up(down_w), out, bits=bits)()
     return _sync_get(out)[0]
+
+
+# ---------------------------------------------------------------------------
+# Runner-door templates (reference: kernelverify/pack/moe_dispatch.py:148-234)
+# ---------------------------------------------------------------------------
+ROUTING_NAME = "kvp_moe_route"
+DISPATCH_NAME = "kvp_moe_dispatch"
+BLOCK = 256
+
+
+def routing_launch(n_tokens: int) -> tuple:
+    """(grid, block): one block per token (the logits sit in LDS)."""
+    return (n_tokens, 1, 1), (BLOCK, 1, 1)
+
+
+def dispatch_launch(d_out: int, n_tokens: int) -> tuple:
+    """(grid, block, rows per block): the single-linear dispatch kernel runs
+    a block per (8 output rows, token)."""
+    rows = 8
+    return ((d_out + rows - 1) // rows, n_tokens, 1), (BLOCK, 1, 1), rows
+
+
+def routing_spec():
+    """Routing template: `specialize()` fills `E`; the top-k width is the
+    outputs' width (the reference's k = 2); d_model is the `d_in_arg` scalar."""
+    from kernelverify_amd.runners import Binding, BindingKind, KernelSpec, LaunchMode, LaunchSpec
+
+    return KernelSpec(
+        source="kvpack:moe_routing E=$E",
+        entry_point=ROUTING_NAME,
+        name=f"{ROUTING_NAME}-E$E",
+        bindings=(Binding(BindingKind.INPUT, "x"),
+                  Binding(BindingKind.INPUT, "router"),
+                  Binding(BindingKind.OUTPUT),
+                  Binding(BindingKind.OUTPUT),
+                  Binding(BindingKind.SCALAR, "d_in_arg", "uint32")),
+        launch=LaunchSpec(grid=("n_tokens", 1, 1), threadgroup=(BLOCK, 1, 1),
+                          mode=LaunchMode.THREADGROUPS),
+    )
+
+
+def dispatch_spec(bits: int | None = None):
+    """Dispatch template: `specialize()` fills `T` and `R` (R is recorded;
+    the library tiles by its own rule). The reference kernel is 4-bit only;
+    ``bits`` fixes another width in the descriptor."""
+    from kernelverify_amd.runners import Binding, BindingKind, KernelSpec, LaunchMode, LaunchSpec
+
+    width = "" if bits is None else f" BITS={int(bits)}"
+    return KernelSpec(
+        source=f"kvpack:moe_dispatch T=$T R=$R{width}",
+        entry_point=DISPATCH_NAME,
+        name=f"{DISPATCH_NAME}-R$R-$T",
+        bindings=(Binding(BindingKind.INPUT, "x"),
+                  Binding(BindingKind.INPUT, "idx"),
+                  Binding(BindingKind.INPUT, "gate"),
+                  Binding(BindingKind.INPUT, "w_q"),
+                  Binding(BindingKind.INPUT, "scales"),
+                  Binding(BindingKind.INPUT, "biases"),
+                  Binding(BindingKind.OUTPUT),
+                  Binding(BindingKind.SCALAR, "d_in_arg", "uint32"),
+                  Binding(BindingKind.SCALAR, "d_out_arg", "uint32")),
+        launch=LaunchSpec(grid=("row_blocks", "n_tokens", 1), threadgroup=(BLOCK, 1, 1),
+                          mode=LaunchMode.THREADGROUPS),
+    )

@@ -126,3 +126,31 @@ def qmv(x: np.ndarray, w_q: np.ndarray, scales: np.ndarray, biases: np.ndarray, 
     run_qmv(dx, dw, ds, db, out, bits=bits)
     hip.synchronize()
     return out.to_host()
+
+
+def kernel_spec():
+    """The runner-door template (reference: kernelverify/pack/wide_qmv.py:218-260).
+
+    A pack-library descriptor with the reference template's compile-time
+    constants: `specialize()` fills `T` (half | float), `BITS`, `M` and `R`;
+    the bindings keep the reference's names and order (x, w_q, scales,
+    biases, out, d_in_arg, d_out_arg). `R` is accepted and recorded; the
+    library tiles by its own rule (`rows_per_wave`). The grid's `row_blocks`
+    extent is informational for the library, which launches its own grid.
+    """
+    from kernelverify_amd.runners import Binding, BindingKind, KernelSpec, LaunchMode, LaunchSpec
+
+    return KernelSpec(
+        source="kvpack:wide_qmv T=$T BITS=$BITS M=$M R=$R",
+        entry_point=KERNEL_NAME,
+        name=f"{KERNEL_NAME}-$BITS bit-M$M-R$R-$T",
+        bindings=(Binding(BindingKind.INPUT, "x"),
+                  Binding(BindingKind.INPUT, "w_q"),
+                  Binding(BindingKind.INPUT, "scales"),
+                  Binding(BindingKind.INPUT, "biases"),
+                  Binding(BindingKind.OUTPUT),
+                  Binding(BindingKind.SCALAR, "d_in_arg", "uint32"),
+                  Binding(BindingKind.SCALAR, "d_out_arg", "uint32")),
+        launch=LaunchSpec(grid=("row_blocks", 1, 1), threadgroup=(WAVE * WAVES_PER_BLOCK, 1, 1),
+                          mode=LaunchMode.THREADGROUPS),
+    )

@@ -1,0 +1,46 @@
+"""The pack gates through the runner door (the reference's
+bench/pack_*.py verify() drivers, here tests/gates/): each must come back
+green, and the quantizer faults of the contract (oracle FAULTS, the
+reference's negative controls, tests/test_pack_verify.py:47-54) must each
+turn the qmv gate red when the kernel is fed the faulted artefact."""
+
+import pytest
+
+from kernelverify_amd.runners import HipRunner
+from oracle.quant_contract import FAULTS
+from tests.gates import pack_kv_attention, pack_moe_dispatch, pack_wide_qmv
+
+pytestmark = pytest.mark.gpu
+
+
+def quiet(*_):
+    pass
+
+
+def test_qmv_gate_green_every_width():
+    """The qmv gate at one of its shapes, every width, M in {1, 4} (the full
+    policy is `python -m tests.gates.pack_wide_qmv`)."""
+    ev = pack_wide_qmv.verify(HipRunner(repeats=1), shapes=[(2560, 2560)], ms=[1, 4], out=quiet)
+    assert ev.cases_run == 16
+    assert ev.ok, [c for s in ev.specializations for c in s.cases if not c.passed] + \
+        [c for c in ev.checks if not c.passed]
+
+
+def test_kv_gate_green():
+    ev = pack_kv_attention.verify(HipRunner(repeats=1), out=quiet)
+    assert ev.cases_run == 9 and ev.ok, [c for s in ev.specializations for c in s.cases
+                                        if not c.passed] + [c for c in ev.checks if not c.passed]
+
+
+def test_moe_gate_green():
+    ev = pack_moe_dispatch.verify(HipRunner(repeats=1), out=quiet)
+    assert ev.cases_run == 12 and ev.ok, [c for s in ev.specializations for c in s.cases
+                                         if not c.passed]
+
+
+@pytest.mark.parametrize("fault", sorted(FAULTS))
+def test_each_quantizer_fault_turns_the_qmv_gate_red(fault):
+    ev = pack_wide_qmv.verify(HipRunner(repeats=1), shapes=[(512, 1024)], bits_list=(4,),
+                              ms=[1], artefact_fault=FAULTS[fault], out=quiet)
+    assert ev.cases_run == 2
+    assert ev.cases_passed == 0, (fault, [c for s in ev.specializations for c in s.cases])
