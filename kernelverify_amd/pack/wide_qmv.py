@@ -18,6 +18,9 @@ large for LDS, staged in chunks). Widths 2, 3, 4 and 8 bits are all served
 
 from __future__ import annotations
 
+import hashlib
+from pathlib import Path
+
 import numpy as np
 
 from kernelverify_amd import lib
@@ -36,6 +39,32 @@ OUT_DTYPES = {"float16": lib.KVP_F16, "float32": lib.KVP_F32}
 def rows_per_wave(m: int) -> int:
     """RW: rows a wave walks together (the VGPR budget of M * RW accumulators)."""
     return 2 if m <= 8 else 1
+
+
+KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h")
+
+
+def kernel_source_sha256() -> str:
+    """sha256 over the qmv kernel sources (the body a routing recording
+    priced; the reference pins the MSL string, routed_windows.py:61-64)."""
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        h.update((Path(__file__).resolve().parents[1] / rel).read_bytes())
+    return h.hexdigest()
+
+
+def should_dispatch(m: int, bits: int, d_out: int, d_in: int) -> bool:
+    """Whether this cell should run on the pack or stay on the vendor GEMM
+    (reference: pack/wide_qmv.py:143-177).
+
+    Every argument is required: routing is a property of the whole (tile
+    width, bit width, shape) cell, read from the measured windows in
+    routed_windows. A shape or width the recording did not price routes
+    nowhere, whatever the kernel supports.
+    """
+    from kernelverify_amd.pack import routed_windows
+
+    return m in routed_windows.window_for(bits, d_out, d_in)
 
 
 def launch_config(d_out: int, m: int) -> tuple:
