@@ -27,6 +27,10 @@
 #include "qmv_core.h"
 
 namespace kvp {
+
+int launch_qmv_mfma(int bits, bool f32_out, const void* x, const uint32_t* wq, const void* s,
+                    const void* b, void* out, int m, int d_out, int d_in, hipStream_t st);
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -749,6 +753,12 @@ int dispatch_m(int m, const void* x, const uint32_t* wq, const void* s, const vo
 template <typename OutT>
 int dispatch_bits(int bits, int m, const void* x, const uint32_t* wq, const void* s,
                   const void* b, void* out, int d_out, int d_in, hipStream_t st) {
+  // Matrix cores for 4/8-bit at M >= 2 (qmv_mfma.hip): their cost does not
+  // grow with M. KVP_QMV_PATH=4 forces them at M = 1, 1..3 the VALU paths.
+  const int path = env_int("KVP_QMV_PATH", 0);
+  const bool fits = (size_t)d_out * d_in / 8 * bits < (size_t(1) << 31);  // 32-bit buffer offsets
+  if ((bits == 4 || bits == 8) && fits && ((path == 0 && m >= 2) || path == 4))
+    return launch_qmv_mfma(bits, sizeof(OutT) == 4, x, wq, s, b, out, m, d_out, d_in, st);
   switch (bits) {
     case 2: return dispatch_m<2, OutT>(m, x, wq, s, b, out, d_out, d_in, st);
     case 3: return dispatch_m<3, OutT>(m, x, wq, s, b, out, d_out, d_in, st);

@@ -12,8 +12,11 @@ M <= 8, 1 above), lanes stream 16-byte units, and codes multiply as exact
 fp16 denormals through V_DOT2_F32_F16. Three kernel paths share that core:
 streaming (M = 1: each wave loads its own activation fragments, no LDS, no
 barrier), resident (x staged once per persistent block) and chunked (x too
-large for LDS, staged in chunks). Widths 2, 3, 4 and 8 bits are all served
-(the reference kernel stops at 4, :140).
+large for LDS, staged in chunks). From M = 2, 4- and 8-bit rows run on the
+matrix cores instead (csrc/qmv_mfma.hip): codes as exact fp16 denormals
+times a block-diagonal activation operand, so the cost no longer grows with
+M. Widths 2, 3, 4 and 8 bits are all served (the reference kernel stops at
+4, :140).
 """
 
 from __future__ import annotations
@@ -41,7 +44,7 @@ def rows_per_wave(m: int) -> int:
     return 2 if m <= 8 else 1
 
 
-KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h")
+KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h", "csrc/qmv_mfma.hip")
 
 
 def kernel_source_sha256() -> str:

@@ -19,7 +19,8 @@ from tests.gates.price_qmv_boundary import classify
 
 # Written out by hand from kernelverify_amd/pack/recordings/
 # qmv-boundary-pricing-mi355x.json: the tile widths at which kvp_qmv beat the
-# vendor fp16 GEMM with the whole ratio interval above 1.
+# vendor fp16 GEMM with the whole ratio interval above 1 (4- and 8-bit run on
+# the matrix cores from M = 2), less the excluded lm_head island.
 EXPECTED_TABLE = {
     (2, 1024, 2560): range(1, 4), (2, 2560, 4096): range(1, 4), (2, 2560, 9728): range(1, 9),
     (2, 4096, 2560): range(1, 3), (2, 4096, 4096): range(1, 4), (2, 4096, 14336): range(1, 9),
@@ -27,12 +28,12 @@ EXPECTED_TABLE = {
     (3, 1024, 2560): range(1, 3), (3, 2560, 4096): range(1, 2), (3, 2560, 9728): range(1, 9),
     (3, 4096, 2560): range(1, 2), (3, 4096, 4096): range(1, 2), (3, 4096, 14336): range(1, 8),
     (3, 9728, 2560): range(1, 2), (3, 14336, 4096): range(1, 3), (3, 151936, 2560): range(1, 2),
-    (4, 1024, 2560): range(1, 5), (4, 2560, 4096): range(1, 4), (4, 2560, 9728): range(1, 9),
-    (4, 4096, 2560): range(1, 4), (4, 4096, 4096): range(1, 4), (4, 4096, 14336): range(1, 9),
-    (4, 9728, 2560): range(1, 4), (4, 14336, 4096): range(1, 6), (4, 151936, 2560): range(1, 4),
-    (8, 1024, 2560): range(1, 3), (8, 2560, 4096): range(1, 2), (8, 2560, 9728): range(1, 10),
-    (8, 4096, 2560): range(1, 2), (8, 4096, 4096): range(1, 3), (8, 4096, 14336): range(1, 11),
-    (8, 9728, 2560): range(1, 3), (8, 14336, 4096): range(1, 3), (8, 151936, 2560): range(1, 3),
+    (4, 1024, 2560): range(1, 9), (4, 2560, 4096): range(1, 7), (4, 2560, 9728): range(1, 12),
+    (4, 4096, 2560): range(1, 9), (4, 4096, 4096): range(1, 9), (4, 4096, 14336): range(1, 17),
+    (4, 9728, 2560): range(1, 9), (4, 14336, 4096): range(1, 9), (4, 151936, 2560): range(1, 6),
+    (8, 1024, 2560): range(1, 9), (8, 2560, 4096): range(1, 7), (8, 2560, 9728): range(1, 12),
+    (8, 4096, 2560): range(1, 9), (8, 4096, 4096): range(1, 7), (8, 4096, 14336): range(1, 17),
+    (8, 9728, 2560): range(1, 5), (8, 14336, 4096): range(1, 7), (8, 151936, 2560): range(1, 5),
 }
 
 
@@ -98,7 +99,9 @@ def test_only_win_with_an_interval_above_one_routes():
 
 def test_should_dispatch_reads_the_windows():
     assert wide_qmv.should_dispatch(1, 4, 14336, 4096)
+    assert wide_qmv.should_dispatch(8, 4, 14336, 4096)
     assert not wide_qmv.should_dispatch(16, 4, 14336, 4096)   # measured LOSS
+    assert not wide_qmv.should_dispatch(8, 4, 151936, 2560)   # measured WIN, excluded island
     assert not wide_qmv.should_dispatch(1, 4, 14336, 4097)    # never priced
     assert not wide_qmv.should_dispatch(1, 5, 14336, 4096)    # unpriced width
     with pytest.raises(TypeError):
