@@ -18,8 +18,10 @@ re-targeted to HIP):
 - ``roofline.achieved`` = algorithmic bytes per launch / ms_per_step, with
   the bytes of ``kernelverify_amd.pack.wide_qmv.algorithmic_bytes``.
 
-The secondary configurations (8-bit, M = 4/8, 4096 x 14336, KV decode, MoE)
-are reported under "secondary" in the same line.
+The other BASELINE configurations ride in the same line: the qmv ones
+(config 1's 4096 x 4096, config 2's 8-bit, M = 4/8 and 4096 x 14336) under
+"secondary", KV decode (configs 3 and 4 and the 32k case) under "kv_decode",
+and the MoE expert layer (config 5) under "moe".
 
 ``--gpus N`` with N > 1 exits: this build measures one GPU.
 """
@@ -330,7 +332,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--secondary", action="store_true", help="also time the secondary qmv configs")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other BASELINE qmv configs (configs 1 and 2 beside the headline)")
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline qmv workload (profiling runs)")
     args = ap.parse_args()
@@ -368,7 +371,7 @@ def main() -> int:
     log(f"[bench] {head.name}: {us:.3f} us/call, {gbs:.1f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)")
 
     secondary = []
-    if args.secondary:
+    if not (args.no_secondary or args.headline_only):
         for d_out, d_in, bits, m in ((4096, 4096, 4, 1), (14336, 4096, 8, 1), (14336, 4096, 4, 4),
                                      (14336, 4096, 4, 8), (4096, 14336, 4, 1)):
             w = QmvWorkload(d_out, d_in, bits, m, seed=1)
