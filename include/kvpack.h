@@ -145,7 +145,8 @@ int kvp_moe_route_logits(const float* logits, uint32_t* idx, float* gate, int n,
  * reference kernel: the reference dispatches per token, :84-138).
  *   offsets int32 [n_experts + 1]: pairs of expert e are perm[offsets[e] ..
  *           offsets[e+1]); perm int32 [n*k]: flat index token*k + slot,
- *           ascending within each expert. Bit-exact and deterministic. */
+ *           ascending within each expert. Bit-exact and deterministic.
+ * n * k <= 8192 (one workgroup holds the pairs). */
 int kvp_moe_permute(const uint32_t* idx, int32_t* offsets, int32_t* perm, int n, int k,
                     int n_experts, void* stream);
 
@@ -169,7 +170,8 @@ int kvp_moe_dispatch(const void* x, const uint32_t* idx, const float* gate,
  * out [n][d_model]. Experts are visited once per step: the (token, slot)
  * pairs are grouped by expert (kvp_moe_permute) so each expert's weights
  * stream from HBM once however many tokens chose it.
- * workspace: kvp_moe_swiglu_workspace_bytes(n, k, n_experts, d_model, d_ffn). */
+ * n * k <= 8192. workspace: kvp_moe_swiglu_workspace_bytes(n, k, n_experts,
+ * d_model, d_ffn). */
 size_t kvp_moe_swiglu_workspace_bytes(int n, int k, int n_experts, int d_model, int d_ffn);
 int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* gate,
                    const uint32_t* gate_wq, const void* gate_scales, const void* gate_biases,

@@ -1,0 +1,90 @@
+// Matrix-core helpers shared by the quantized GEMV kernels (qmv_mfma.hip,
+// moe.hip): V_MFMA_F32_16X16X32_F16 with weight codes as exact fp16
+// denormals (c * 2^-24) in the B operand and activations in the A operand.
+//
+// Operand layouts of one 16x16x32 instruction (lane l of a 64-lane wave):
+//   A: row l % 16, k-octet l / 16 (8 fp16);  B: k-octet l / 16, column l % 16;
+//   D: rows 4 (l / 16) .. + 3, column l % 16 (4 fp32).
+// The code masks yield codes in pair order, (c_j, c_j+4) per 4-bit word and
+// (c0, c2), (c1, c3) per 8-bit word; activations are staged in that order.
+#pragma once
+
+#include <stdlib.h>
+
+#include "common.h"
+
+namespace kvp {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads as zero
+
+// Raw buffer resource over [p, p + bytes): reads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BITS, int MT>
+struct MfmaShape {
+  static constexpr int kNB = 16 / MT;            // row blocks of A (independent groups per step)
+  static constexpr int kOPB = 4 / kNB;           // k-octets per block
+  static constexpr int kT = 2 * kNB;             // MFMAs per step
+  static constexpr int kCPL = 16 * kNB;          // codes per lane per step
+  static constexpr int kWPL = kCPL * BITS / 32;  // code words per lane per step
+  static constexpr int kGroupBytes = 8 * BITS;   // one 64-code group of a row
+  static constexpr int kSlotsPerGroup = 9;       // 8 slots of 8 codes + 1 pad slot (banks)
+  // Steps in flight per wave: about 4 KiB of weights per wave (deeper rings
+  // cost the VGPRs that let two 8-wave blocks share a CU).
+  static constexpr int kPD = (4096 / (64 * kWPL * 4)) < 2 ? 2 : 4096 / (64 * kWPL * 4);
+};
+
+// Pair order of one 8-code slot: operand position p holds x[slot_src(p)].
+template <int BITS>
+__device__ __forceinline__ int slot_src(int p) {
+  // 4-bit (w >> 4j) & 0x000F000F -> (c_j, c_j+4); 8-bit (w >> 8j) & 0x00FF00FF
+  // over two words -> (c0, c2), (c1, c3), (c4, c6), (c5, c7).
+  if constexpr (BITS == 4) return (p & 1) ? (p >> 1) + 4 : (p >> 1);
+  else return (p < 4 ? 0 : 4) + ((p & 1) ? 2 : 0) + ((p >> 1) & 1);
+}
+
+// The B operand of MFMA t from this lane's code words.
+template <int BITS>
+__device__ __forceinline__ f16x8 code_operand(const uint32_t* w, int t) {
+  u32x4 r;
+  if constexpr (BITS == 4) {
+    const uint32_t v = w[t];
+    r.x = v & 0x000F000Fu;
+    r.y = (v >> 4) & 0x000F000Fu;
+    r.z = (v >> 8) & 0x000F000Fu;
+    r.w = (v >> 12) & 0x000F000Fu;
+  } else {
+    const uint32_t v0 = w[2 * t], v1 = w[2 * t + 1];
+    r.x = v0 & 0x00FF00FFu;
+    r.y = (v0 >> 8) & 0x00FF00FFu;
+    r.z = v1 & 0x00FF00FFu;
+    r.w = (v1 >> 8) & 0x00FF00FFu;
+  }
+  return __builtin_bit_cast(f16x8, r);
+}
+
+// Eight fp16 activations in natural order -> the slot's operand order.
+template <int BITS>
+__device__ __forceinline__ u32x4 to_slot_order(u32x4 natural) {
+  const f16x8 nat = __builtin_bit_cast(f16x8, natural);
+  f16x8 op;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) op[p] = nat[slot_src<BITS>(p)];
+  return __builtin_bit_cast(u32x4, op);
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// accesses, not for its weight loads in flight (a fence would drain those).
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // compiler ordering only, no wait
+  __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0); vmcnt, expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+}  // namespace kvp

@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "mfma_core.h"
 #include "qmv_core.h"
 
 namespace kvp {
@@ -31,6 +32,7 @@ constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxK = 32;
+constexpr int kPermuteTile = 8192;  // routed pairs (n * k) one permutation holds
 
 // ---------------------------------------------------------------------------
 // Routing
@@ -164,49 +166,66 @@ __global__ __launch_bounds__(1024) void permute_kernel(const uint32_t* __restric
                                                        int n_experts) {
   __shared__ int32_t cnt[kMaxExperts];
   __shared__ int32_t off[kMaxExperts + 1];
-  __shared__ uint32_t tile[1024];
+  __shared__ int32_t act_pos[kMaxExperts];
+  __shared__ uint32_t tile[kPermuteTile];
   for (int e = threadIdx.x; e < n_experts; e += blockDim.x) cnt[e] = 0;
-  // A pair naming no valid expert is never placed: its slot stays -1 and the
-  // scatter skips it.
-  if (slot_of)
-    for (int i = threadIdx.x; i < pairs; i += blockDim.x) slot_of[i] = -1;
+  for (int i = threadIdx.x; i < pairs; i += blockDim.x) tile[i] = idx[i];
   __syncthreads();
   for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
-    const uint32_t e = idx[i];
+    const uint32_t e = tile[i];
     if (e < (uint32_t)n_experts) atomicAdd(&cnt[e], 1);  // counts are order-free
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0, act = 0;
-    for (int e = 0; e < n_experts; ++e) {
-      off[e] = run;
-      run += cnt[e];
-      if (cnt[e] > 0 && active) active[1 + act++] = e;
+  // Exclusive scans of the counts and of the routed flags: wave 0, each lane
+  // a contiguous run of experts, then a scan of the lane totals.
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    const int per = (n_experts + kWave - 1) / kWave;
+    const int e0 = min(lane * per, n_experts), e1 = min(e0 + per, n_experts);
+    int c = 0, f = 0;
+    for (int e = e0; e < e1; ++e) {
+      c += cnt[e];
+      f += cnt[e] > 0;
     }
-    off[n_experts] = run;
-    if (active) active[0] = act;
+    int ci = c, fi = f;  // inclusive scans over lanes
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int cu = __shfl_up(ci, d, kWave), fu = __shfl_up(fi, d, kWave);
+      if (lane >= d) {
+        ci += cu;
+        fi += fu;
+      }
+    }
+    int run = ci - c, act = fi - f;
+    for (int e = e0; e < e1; ++e) {
+      off[e] = run;
+      act_pos[e] = act;
+      run += cnt[e];
+      act += cnt[e] > 0;
+    }
+    if (lane == kWave - 1) {
+      off[n_experts] = ci;
+      if (active) active[0] = fi;
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e <= n_experts; e += blockDim.x) offsets[e] = off[e];
-  // Stable placement: one thread per expert walks the pairs in flat order.
-  for (int e0 = 0; e0 < n_experts; e0 += blockDim.x) {
-    const int e = e0 + threadIdx.x;
-    int pos = e < n_experts ? off[e] : 0;
-    for (int base = 0; base < pairs; base += 1024) {
-      const int m = min(1024, pairs - base);
-      __syncthreads();
-      for (int i = threadIdx.x; i < m; i += blockDim.x) tile[i] = idx[base + i];
-      __syncthreads();
-      if (e < n_experts) {
-        for (int i = 0; i < m; ++i) {
-          if (tile[i] == (uint32_t)e) {
-            perm[pos] = base + i;
-            if (slot_of) slot_of[base + i] = pos;
-            ++pos;
-          }
-        }
-      }
+  if (active)
+    for (int e = threadIdx.x; e < n_experts; e += blockDim.x)
+      if (cnt[e] > 0) active[1 + act_pos[e]] = e;
+  // Stable placement: a pair's rank among the earlier pairs of its expert.
+  // A pair naming no valid expert is never placed (slot -1: the scatter
+  // skips it).
+  for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
+    const uint32_t e = tile[i];
+    int pos = -1;
+    if (e < (uint32_t)n_experts) {
+      int rank = 0;
+      for (int j = 0; j < i; ++j) rank += tile[j] == e;
+      pos = off[e] + rank;
+      perm[pos] = i;
     }
+    if (slot_of) slot_of[i] = pos;
   }
 }
 
@@ -458,6 +477,244 @@ __global__ __launch_bounds__(kBlock) void expert_f32_kernel(ExpertArgs a) {
   }
 }
 
+// Matrix-core expert GEMV (4/8-bit codes), the qmv_mfma layout per expert:
+// a block is one 16-row tile of one routed expert; the four waves split the
+// tile's groups; A rows are up to four activation rows of the expert's
+// pairs, block-diagonal over the four k-octets so each lane quarter walks
+// its own 64-code group. fp16 activations (gate/up) give four tokens per
+// pass; the fp32 hidden state of the down projection enters as two tokens
+// per pass, each as an exact fp16 hi/lo pair (h * 2^-E = hi + lo to 22 bits,
+// E a power-of-two shift that keeps every value inside fp16), so no fp16
+// intermediate replaces h (contract C1): D(hi) + D(lo) is the fp32 product.
+// SwiGLU computes the gate and up tiles of the same rows together.
+constexpr int kEMT = 4;                              // A rows per pass
+constexpr int kEGroupSlots = 9;                      // 8 operand slots + 1 pad (banks)
+
+template <int BITS, bool SWIGLU>
+struct ExpertStep {
+  uint32_t w[SWIGLU ? 2 : 1][MfmaShape<BITS, kEMT>::kWPL];
+  uint32_t s[SWIGLU ? 2 : 1], b[SWIGLU ? 2 : 1];
+};
+
+// KQ waves share one tile's steps (KQ = 4: one tile per block, for long
+// rows) or each wave runs all of its own tile's steps (KQ = 1: four tiles per
+// block share one staging of the activations, for short rows).
+template <int BITS, bool SWIGLU, bool F32IN, int KQ>
+__global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
+  using S = MfmaShape<BITS, kEMT>;
+  constexpr int NP = SWIGLU ? 2 : 1;            // projections per tile
+  constexpr int TPP = F32IN ? kEMT / 2 : kEMT;  // tokens per pass
+  constexpr int TB = kWaves / KQ;               // tiles per block
+  constexpr int RS = KQ == 1 ? 4 : 2;           // steps in flight per wave
+  extern __shared__ __align__(16) uint4 lds[];
+  __shared__ float red[kWaves][NP][kEMT][16];
+  const int act = blockIdx.y;
+  if (act >= a.active[0]) return;  // block-uniform
+  const int e = a.active[1 + act];
+  const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
+  const int G = a.d_in / 64;                 // a multiple of 4 (checked by the launcher)
+  const int steps = G / S::kNB;
+  const int m_stride = G * kEGroupSlots + 1;  // slots per A row
+  uint4* xs = lds;
+  uint4* zeros = lds + kEMT * m_stride;
+  float* sums = reinterpret_cast<float*>(zeros + S::kT);  // [G][kEMT]
+  float* mult = sums + G * kEMT;                           // [G][kEMT] (fp32 input only)
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int tl = wave / KQ, kq = wave - tl * KQ;
+  const int n = lane & 15, h = lane >> 4;  // blk = h (MT = 4: one octet per block)
+  const int row = (blockIdx.x * TB + tl) * 16 + n;
+  const bool row_ok = row < a.d_out;
+  const uint32_t row_bytes = (uint32_t)a.d_in * BITS / 8;
+  const size_t erow = (size_t)e * a.d_out;
+  const uint32_t wbytes = (uint32_t)(a.d_out * row_bytes), sbytes = (uint32_t)(a.d_out * G * 2);
+  __amdgpu_buffer_rsrc_t wr[NP], sr[NP], br[NP];
+  wr[0] = rsrc(a.wq0 + erow * (row_bytes / 4), wbytes);
+  sr[0] = rsrc(a.s0 + erow * G, sbytes);
+  br[0] = rsrc(a.b0 + erow * G, sbytes);
+  if constexpr (SWIGLU) {
+    wr[1] = rsrc(a.wq1 + erow * (row_bytes / 4), wbytes);
+    sr[1] = rsrc(a.s1 + erow * G, sbytes);
+    br[1] = rsrc(a.b1 + erow * G, sbytes);
+  }
+  const uint32_t code_base = row_ok ? (uint32_t)row * row_bytes + h * S::kGroupBytes : kOutOfRange;
+  const uint32_t sb_base = row_ok ? ((uint32_t)row * G + h) * 2 : kOutOfRange;
+  const bool a_live = (n >> 2) == h;  // A row n is (block n / 4, x row n % 4)
+  const uint4* a_base = a_live ? xs + (n & 3) * m_stride + h * kEGroupSlots : zeros;
+  const uint32_t a_mul = a_live ? 1u : 0u;
+
+  auto load = [&](ExpertStep<BITS, SWIGLU>& R, int st) {
+    const bool live = st < steps;  // wave-uniform
+    const uint32_t co = code_base + (live ? (uint32_t)st * 4 * S::kGroupBytes : kOutOfRange);
+    const uint32_t so = sb_base + (live ? (uint32_t)st * 4 * 2 : kOutOfRange);
+#pragma unroll
+    for (int pj = 0; pj < NP; ++pj) {
+#pragma unroll
+      for (int i = 0; i < S::kWPL; i += 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr[pj], co + 4 * i, 0, 0);
+        R.w[pj][i] = v.x; R.w[pj][i + 1] = v.y; R.w[pj][i + 2] = v.z; R.w[pj][i + 3] = v.w;
+      }
+      R.s[pj] = __builtin_amdgcn_raw_buffer_load_b16(sr[pj], so, 0, 0);
+      R.b[pj] = __builtin_amdgcn_raw_buffer_load_b16(br[pj], so, 0, 0);
+    }
+  };
+  // A wave's steps are kq, kq + KQ, ...; RS of them are in flight at a time
+  // (the first RS are requested before anything else).
+  const int spw = (steps - kq + KQ - 1) / KQ;  // wave-uniform
+  ExpertStep<BITS, SWIGLU> R[RS];
+#pragma unroll
+  for (int j = 0; j < RS; ++j) load(R[j], kq + KQ * j);
+  if (threadIdx.x < S::kT) zeros[threadIdx.x] = uint4{0, 0, 0, 0};
+  bool fresh = true;  // R holds this wave's first RS steps
+
+  for (int q0 = p0; q0 < p1; q0 += TPP) {  // block-uniform passes over the expert's pairs
+    const int nt = min(TPP, p1 - q0);
+    if constexpr (!F32IN) {
+      // Stage: item (token row m, group g), one thread each.
+      for (int it = threadIdx.x; it < kEMT * G; it += kBlock) {
+        const int m = it / G, g = it - m * G;
+        uint4* dst = xs + m * m_stride + g * kEGroupSlots;
+        float sum = 0.0f;
+        u32x4 v[8];
+        const bool live = m < nt;
+        const int tok = live ? a.perm[q0 + m] / a.k : 0;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.x + (size_t)tok * a.d_in + g * 64);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          v[q] = live ? *reinterpret_cast<const u32x4*>(src + 4 * q) : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const u32x4 ow = to_slot_order<BITS>(v[q]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sum = dot2(ow[j], 0x3C003C00u, sum);
+          dst[q] = uint4{ow.x, ow.y, ow.z, ow.w};
+        }
+        sums[g * kEMT + m] = sum;
+      }
+    } else {
+      // Stage: item (token, group, quarter of 16 values), four lanes per
+      // (token, group) that agree on its shift; each writes its two slots of
+      // the hi row (2 tk) and the lo row (2 tk + 1).
+      for (int it = threadIdx.x; it < TPP * G * 4; it += kBlock) {
+        const int qq = it & 3, tg = it >> 2;
+        const int tk = tg / G, g = tg - tk * G;
+        const bool live = tk < nt;
+        const float* src = a.xf + (size_t)(q0 + (live ? tk : 0)) * a.d_in + g * 64 + 16 * qq;
+        float hv[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+          const float4 v = live ? *reinterpret_cast<const float4*>(src + i) : float4{0, 0, 0, 0};
+          hv[i] = v.x; hv[i + 1] = v.y; hv[i + 2] = v.z; hv[i + 3] = v.w;
+        }
+        float mx = 0.0f, tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          mx = fmaxf(mx, fabsf(hv[i]));
+          tot += hv[i];
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 4));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 4));
+        tot += __shfl_xor(tot, 1, 4);
+        tot += __shfl_xor(tot, 2, 4);
+        // Shift so the largest |h| stays below 2^14: hi and lo then fit fp16.
+        const int ex = mx > 0.0f ? max(0, ilogbf(mx) - 13) : 0;
+        const float inv = ldexpf(1.0f, -ex);
+        uint4* dhi = xs + (2 * tk) * m_stride + g * kEGroupSlots + 2 * qq;
+        uint4* dlo = dhi + m_stride;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          f16x8 hi8, lo8;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float hs = hv[8 * q + j] * inv;
+            const _Float16 hi = (_Float16)hs;
+            hi8[j] = hi;
+            lo8[j] = (_Float16)(hs - (float)hi);
+          }
+          const u32x4 oh = to_slot_order<BITS>(__builtin_bit_cast(u32x4, hi8));
+          const u32x4 ol = to_slot_order<BITS>(__builtin_bit_cast(u32x4, lo8));
+          dhi[q] = uint4{oh.x, oh.y, oh.z, oh.w};
+          dlo[q] = uint4{ol.x, ol.y, ol.z, ol.w};
+        }
+        if (qq == 0) {  // b * sum(h) rides on the hi row; both rows scale back by 2^E
+          sums[g * kEMT + 2 * tk] = tot;
+          sums[g * kEMT + 2 * tk + 1] = 0.0f;
+          mult[g * kEMT + 2 * tk] = mult[g * kEMT + 2 * tk + 1] = ldexpf(1.0f, ex);
+        }
+      }
+    }
+    lds_barrier();
+
+    f32x4 acc[NP];
+#pragma unroll
+    for (int pj = 0; pj < NP; ++pj) acc[pj] = f32x4{0, 0, 0, 0};
+    auto step = [&](const ExpertStep<BITS, SWIGLU>& Rs, int st) {
+      const int g = st * S::kNB + h;  // this lane's group (D rows and codes alike)
+      const uint4* a_src = a_base + a_mul * (uint32_t)(st * S::kNB * kEGroupSlots);
+      const f32x4 sm = *reinterpret_cast<const f32x4*>(sums + g * kEMT);
+      f32x4 mu = {1.0f, 1.0f, 1.0f, 1.0f};
+      if constexpr (F32IN) mu = *reinterpret_cast<const f32x4*>(mult + g * kEMT);
+#pragma unroll
+      for (int pj = 0; pj < NP; ++pj) {
+        f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < S::kT; ++t)
+          d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_src[t]),
+                                                     code_operand<BITS>(Rs.w[pj], t), d, 0, 0, 0);
+        const float sc = f16_bits_to_f32((uint16_t)Rs.s[pj]) * 16777216.0f;  // c * 2^-24
+        const float bi = f16_bits_to_f32((uint16_t)Rs.b[pj]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[pj][r] = fmaf(sc * mu[r], d[r], fmaf(bi, sm[r], acc[pj][r]));
+      }
+    };
+    for (int jb = 0; jb < spw; jb += RS) {  // wave-uniform
+      if (!fresh) {
+#pragma unroll
+        for (int j = 0; j < RS; ++j) load(R[j], kq + KQ * (jb + j));
+      }
+      fresh = false;
+#pragma unroll
+      for (int j = 0; j < RS; ++j)
+        if (jb + j < spw) step(R[j], kq + KQ * (jb + j));
+    }
+    // Merge the four row blocks (other groups, same A rows), then the waves.
+#pragma unroll
+    for (int pj = 0; pj < NP; ++pj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[pj][r] += __shfl_xor(acc[pj][r], 16);
+        acc[pj][r] += __shfl_xor(acc[pj][r], 32);
+      }
+    if (h == 0) {
+#pragma unroll
+      for (int pj = 0; pj < NP; ++pj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][pj][r][n] = acc[pj][r];
+    }
+    __syncthreads();
+    if (threadIdx.x < TB * TPP * 16) {
+      const int tt = threadIdx.x / (TPP * 16), tk = (threadIdx.x >> 4) % TPP, nn = threadIdx.x & 15;
+      const int orow = (blockIdx.x * TB + tt) * 16 + nn;
+      float v[NP];
+#pragma unroll
+      for (int pj = 0; pj < NP; ++pj) {
+        v[pj] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KQ; ++w) {
+          const int ww = tt * KQ + w;
+          if constexpr (F32IN) v[pj] += red[ww][pj][2 * tk][nn] + red[ww][pj][2 * tk + 1][nn];
+          else v[pj] += red[ww][pj][tk][nn];
+        }
+      }
+      float out = v[0];
+      if constexpr (SWIGLU) out = silu(v[0]) * v[1];
+      if (tk < nt && orow < a.d_out) a.y[(size_t)(q0 + tk) * a.d_out + orow] = out;
+    }
+    __syncthreads();  // red and the staged rows are reused by the next pass
+  }
+}
+
 // out[t][d] = sum_s gate[t][s] * y[slot_of[t*k + s]][d], s in order.
 template <typename OutT>
 __global__ __launch_bounds__(kBlock) void scatter_kernel(const float* __restrict__ y,
@@ -572,6 +829,29 @@ template <int BITS>
 int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f32_input,
                    hipStream_t st) {
   using Gm = Geom<BITS>;
+  const int G = a.d_in / 64;
+  if constexpr (BITS == 4 || BITS == 8) {
+    // Matrix cores: four groups per step, at most 16 steps (d_in <= 4096).
+    if (G % 4 == 0 && G <= 64 && getenv("KVP_MOE_VALU") == nullptr) {
+      const size_t lds = ((size_t)kEMT * (G * kEGroupSlots + 1) + 8) * 16 + (size_t)G * kEMT * 8;
+      const int tiles = (a.d_out + 15) / 16;
+      // Short rows (at most 4 steps of 4 groups per tile): one
+      // wave per tile, four tiles per block; longer rows: four waves per tile.
+      const bool short_rows = G / 4 <= 4;
+      const dim3 grid(short_rows ? (tiles + 3) / 4 : tiles, max_active);
+#define KVP_EXPERT(SW, F32, KQ)                                                               \
+  hipLaunchKernelGGL((expert_mfma_kernel<BITS, SW, F32, KQ>), grid, dim3(kBlock), lds, st, a)
+      if (f32_input) {
+        if (short_rows) KVP_EXPERT(false, true, 1); else KVP_EXPERT(false, true, 4);
+      } else if (swiglu_f16) {
+        if (short_rows) KVP_EXPERT(true, false, 1); else KVP_EXPERT(true, false, 4);
+      } else {
+        if (short_rows) KVP_EXPERT(false, false, 1); else KVP_EXPERT(false, false, 4);
+      }
+#undef KVP_EXPERT
+      return check_launch("kvp_moe expert gemv (matrix cores)");
+    }
+  }
   const dim3 grid((a.d_out + kRowsPerBlock - 1) / kRowsPerBlock, max_active);
   if (f32_input) {
     hipLaunchKernelGGL(expert_f32_kernel<BITS>, grid, dim3(kBlock), 0, st, a);
@@ -651,6 +931,8 @@ extern "C" int kvp_moe_permute(const uint32_t* idx, int32_t* offsets, int32_t* p
   KVP_REQUIRE(idx && offsets && perm, "kvp_moe_permute: null pointer argument");
   KVP_REQUIRE(n >= 1 && k >= 1 && n_experts >= 1 && n_experts <= kMaxExperts,
               "kvp_moe_permute: n=%d k=%d n_experts=%d", n, k, n_experts);
+  KVP_REQUIRE((long long)n * k <= kPermuteTile, "kvp_moe_permute: n*k=%lld above %d",
+              (long long)n * k, kPermuteTile);
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), idx,
                      offsets, perm, nullptr, nullptr, n * k, n_experts);
   return check_launch("kvp_moe_permute");
@@ -713,6 +995,8 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
               "kvp_moe_swiglu: null pointer argument");
   KVP_REQUIRE(n >= 1 && k >= 1 && k <= kMaxK && n_experts >= 1 && n_experts <= kMaxExperts,
               "kvp_moe_swiglu: n=%d k=%d n_experts=%d", n, k, n_experts);
+  KVP_REQUIRE((long long)n * k <= kPermuteTile, "kvp_moe_swiglu: n*k=%lld above %d",
+              (long long)n * k, kPermuteTile);
   KVP_REQUIRE(out_dtype == KVP_F16 || out_dtype == KVP_F32, "kvp_moe_swiglu: out_dtype=%d",
               out_dtype);
   if (int rc = check_expert_dims("kvp_moe_swiglu (gate/up)", d_model, d_ffn, bits)) return rc;

@@ -27,70 +27,16 @@
 // (group, x row) beside it; lanes outside their block read a zero slot.
 // Blocks are one 16-row tile; their waves split the tile's steps and merge
 // the partial sums through LDS at the end, in a fixed order (deterministic).
-#include <stdlib.h>
-
-#include "common.h"
+#include "mfma_core.h"
 
 namespace kvp {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 namespace {
 
 constexpr int kMfmaStageBytes = 64 * 1024;  // x chunk budget per block
-constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset that reads as zero
 
 int env_int(const char* name, int fallback) {
   const char* v = getenv(name);
   return v ? atoi(v) : fallback;
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-template <int BITS, int MT>
-struct MfmaShape {
-  static constexpr int kNB = 16 / MT;            // row blocks of A (independent groups per step)
-  static constexpr int kOPB = 4 / kNB;           // k-octets per block
-  static constexpr int kT = 2 * kNB;             // MFMAs per step
-  static constexpr int kCPL = 16 * kNB;          // codes per lane per step
-  static constexpr int kWPL = kCPL * BITS / 32;  // code words per lane per step
-  static constexpr int kGroupBytes = 8 * BITS;   // one 64-code group of a row
-  static constexpr int kSlotsPerGroup = 9;       // 8 slots of 8 codes + 1 pad slot (banks)
-  // Steps in flight per wave: about 4 KiB of weights per wave (deeper rings
-  // cost the VGPRs that let two 8-wave blocks share a CU).
-  static constexpr int kPD = (4096 / (64 * kWPL * 4)) < 2 ? 2 : 4096 / (64 * kWPL * 4);
-};
-
-// Pair order of one 8-code slot: position p of the operand holds x[kOrder[p]].
-template <int BITS>
-__device__ __forceinline__ int slot_src(int p) {
-  // 4-bit (w >> 4j) & 0x000F000F -> (c_j, c_j+4); 8-bit (w >> 8j) & 0x00FF00FF
-  // over two words -> (c0, c2), (c1, c3), (c4, c6), (c5, c7).
-  if constexpr (BITS == 4) return (p & 1) ? (p >> 1) + 4 : (p >> 1);
-  else return (p < 4 ? 0 : 4) + ((p & 1) ? 2 : 0) + ((p >> 1) & 1);
-}
-
-// The B operand of MFMA t from this lane's code words.
-template <int BITS>
-__device__ __forceinline__ f16x8 code_operand(const uint32_t* w, int t) {
-  u32x4 r;
-  if constexpr (BITS == 4) {
-    const uint32_t v = w[t];
-    r.x = v & 0x000F000Fu;
-    r.y = (v >> 4) & 0x000F000Fu;
-    r.z = (v >> 8) & 0x000F000Fu;
-    r.w = (v >> 12) & 0x000F000Fu;
-  } else {
-    const uint32_t v0 = w[2 * t], v1 = w[2 * t + 1];
-    r.x = v0 & 0x00FF00FFu;
-    r.y = (v0 >> 8) & 0x00FF00FFu;
-    r.z = v1 & 0x00FF00FFu;
-    r.w = (v1 >> 8) & 0x00FF00FFu;
-  }
-  return __builtin_bit_cast(f16x8, r);
 }
 
 template <int BITS, int MT>
@@ -127,25 +73,12 @@ __device__ __forceinline__ void mfma_commit(const u32x4 (&v)[8], int M, int kc, 
   uint4* dst = xs + min(m, M - 1) * m_stride_slots + gl * MfmaShape<BITS, MT>::kSlotsPerGroup;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const f16x8 nat = __builtin_bit_cast(f16x8, v[q]);
-    f16x8 op;
-#pragma unroll
-    for (int p = 0; p < 8; ++p) op[p] = nat[slot_src<BITS>(p)];
-    const u32x4 ow = __builtin_bit_cast(u32x4, op);
+    const u32x4 ow = to_slot_order<BITS>(v[q]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) sum = dot2(ow[j], 0x3C003C00u, sum);
     if (m < M) dst[q] = uint4{ow.x, ow.y, ow.z, ow.w};
   }
   xsum[gl * 16 + m] = sum;
-}
-
-// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
-// accesses, not for its weight loads in flight (a fence would drain those).
-__device__ __forceinline__ void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // compiler ordering only, no wait
-  __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0); vmcnt, expcnt untouched
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // A block is TB row tiles of 16 rows; each tile's steps are split over KQ

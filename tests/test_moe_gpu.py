@@ -29,7 +29,7 @@ from oracle.extensions import (
 )
 from oracle.inputs import moe_case
 from oracle.native_ops import _moe_route
-from oracle.quant_contract import QuantContract, canonical_quantize
+from oracle.quant_contract import QuantContract, canonical_quantize, dequantize
 from oracle.verify import judge, moe_inputs, verify_output
 
 pytestmark = pytest.mark.gpu
@@ -210,3 +210,30 @@ def test_swiglu_every_width(bits):
     out = run_swiglu(x, mats, idx, gate, bits)
     v = judge_swiglu(x, mats, idx, gate, out, None)
     assert v.ok, (bits, v)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_swiglu_hidden_state_beyond_fp16_range(bits):
+    """x ~ N(0, 600^2): the fp32 hidden state exceeds 65504, so the down
+    projection's hi/lo fp16 operands must be range-shifted by an exact power
+    of two (the matrix-core path) and still match the fp64 reference."""
+    x, mats, logits = swiglu_case(4, 16, 512, 256, bits, seed=40 + bits)
+    x = (x.astype(np.float32) * 600.0).astype(np.float16)
+    idx, gate = route_topk(logits, 4)
+    g_art, u_art = mats["gate"][3][idx[0, 0]], mats["up"][3][idx[0, 0]]
+    x0 = x[0].astype(np.float64)
+    g, u = x0 @ dequantize(g_art, np.float64).T, x0 @ dequantize(u_art, np.float64).T
+    assert np.abs(g / (1 + np.exp(-np.clip(g, -80, 80))) * u).max() > 65504  # as the name says
+    out = run_swiglu(x, mats, idx, gate, bits, "float32")
+    v = judge_swiglu(x, mats, idx, gate, out, None, "float32")
+    assert v.ok, (bits, v)
+
+
+def test_swiglu_group_count_off_the_matrix_core_tiling():
+    """d_ffn = 320 (five groups, not a multiple of four): the down projection
+    takes the VALU kernel; the result is the same operator."""
+    x, mats, logits = swiglu_case(3, 16, 512, 320, 4, seed=9)
+    idx, gate = route_topk(logits, 4)
+    out = run_swiglu(x, mats, idx, gate, 4)
+    v = judge_swiglu(x, mats, idx, gate, out, None)
+    assert v.ok, v
