@@ -38,9 +38,9 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "e5eebffd145cd3b83bd4952b4fb0eae7e74fda369348118108cb5b78d02a47f4"
+RECORDING_SHA256 = "6468a849ef55ef35fc29a84fc321ba0b79afc92ac0a1a88b180def73e464dcff"
 
-KERNEL_SOURCE_SHA256 = "5b2068b3d4122179e5c7b7815a7f20c375f122f0b1d74efa7877842a5c4fd37f"
+KERNEL_SOURCE_SHA256 = "701eba9f3d56faf50625aa3a6e5b8a5e4b46346ad2b1d3e8d4a38c13fe47cea5"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
 

@@ -44,7 +44,7 @@ def rows_per_wave(m: int) -> int:
     return 2 if m <= 8 else 1
 
 
-KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h", "csrc/qmv_mfma.hip")
+KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h", "csrc/qmv_mfma.hip", "csrc/mfma_core.h")
 
 
 def kernel_source_sha256() -> str:
