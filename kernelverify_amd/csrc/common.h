@@ -59,16 +59,57 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 }
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
   return v;
+}
+
+// DPP lane moves within 16-lane rows (bound_ctrl: lanes without a source
+// read zero), and the row-wide reductions built from them: after four steps
+// every lane of a row holds the row's result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141;  // row_half_mirror
+constexpr int kRowMirror = 0x140;   // row_mirror
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kQuadSwap1>(v));
+  v = fmaxf(v, dpp_f<kQuadSwap2>(v));
+  v = fmaxf(v, dpp_f<kHalfMirror>(v));
+  return fmaxf(v, dpp_f<kRowMirror>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<kQuadSwap1>(v);
+  v += dpp_f<kQuadSwap2>(v);
+  v += dpp_f<kHalfMirror>(v);
+  return v + dpp_f<kRowMirror>(v);
+}
+__device__ __forceinline__ int row16_max_i(int v) {
+  v = max(v, dpp_i<kQuadSwap1>(v));
+  v = max(v, dpp_i<kQuadSwap2>(v));
+  v = max(v, dpp_i<kHalfMirror>(v));
+  return max(v, dpp_i<kRowMirror>(v));
+}
+
+// Sum over the 64 lanes, the same value in every lane: DPP steps within each
+// 16-lane row, then the four row sums read as scalars.
+__device__ __forceinline__ float wave_sum(float v) {
+  const int r = __builtin_bit_cast(int, row16_sum(v));
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 48)));
 }
 
 // Compiler-only barrier: keeps LDS reads of one unrolled step from being

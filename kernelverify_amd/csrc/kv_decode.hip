@@ -439,38 +439,6 @@ __device__ __forceinline__ f16x8 codes8_f16(const uint32_t* w) {
 // same (bit-identical) result.
 // (Every source lane of these patterns lies inside the row, so bound_ctrl's
 // zero fill never applies; it spares the old-value initialisation.)
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float,
-                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
-}
-constexpr int kQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]
-constexpr int kQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]
-constexpr int kHalfMirror = 0x141;  // row_half_mirror
-constexpr int kRowMirror = 0x140;   // row_mirror
-
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<kQuadSwap1>(v));
-  v = fmaxf(v, dpp_f<kQuadSwap2>(v));
-  v = fmaxf(v, dpp_f<kHalfMirror>(v));
-  return fmaxf(v, dpp_f<kRowMirror>(v));
-}
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_f<kQuadSwap1>(v);
-  v += dpp_f<kQuadSwap2>(v);
-  v += dpp_f<kHalfMirror>(v);
-  return v + dpp_f<kRowMirror>(v);
-}
-__device__ __forceinline__ int row16_max_i(int v) {
-  v = max(v, dpp_i<kQuadSwap1>(v));
-  v = max(v, dpp_i<kQuadSwap2>(v));
-  v = max(v, dpp_i<kHalfMirror>(v));
-  return max(v, dpp_i<kRowMirror>(v));
-}
 __device__ __forceinline__ float lane_value(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }

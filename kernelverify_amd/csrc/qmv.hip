@@ -633,6 +633,126 @@ __global__ __launch_bounds__(kBlock) void qmv_stream_kernel(
   finish_set<RW, M, OutT>(acc, set, d_out, lane, out);
 }
 
+// ---------------------------------------------------------------------------
+// Persistent path (M = 1): a fixed grid of waves, each walking row sets
+// wave, wave + n_waves, ... Its lane's activation units stay in registers,
+// already in pair order with their sums, for every row it serves; the
+// weights stream through a ring of PD row sets in flight; each row's 64-lane
+// sum is four DPP steps per 16-lane row and one combination of the rows.
+// ---------------------------------------------------------------------------
+template <int BITS, int RW, int UPL>
+struct PersistSet {
+  uint32_t w[UPL][RW][Geom<BITS>::kUnitWords];
+  uint32_t s[UPL][RW], b[UPL][RW];  // fp16 bits of the unit's group scale and bias
+};
+
+template <int BITS, int RW, int UPL, int PD, typename OutT>
+__global__ __launch_bounds__(kBlock) void qmv_persist_kernel(
+    const f16* __restrict__ x, const uint32_t* __restrict__ wq,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    OutT* __restrict__ out, int d_in, int d_out) {
+  using G = Geom<BITS>;
+  constexpr int kXW = G::kUnitCodes / 2;  // activation words (natural fp16 pairs) of a unit
+  constexpr uint32_t kOOR = 0x80000000u;  // buffer offset that reads as zero
+  constexpr int kUnitsPerGroup = 64 / G::kUnitCodes;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wg = blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int n_waves = gridDim.x * kWavesPerBlock;
+  const int units = d_in / G::kUnitCodes;
+  const int groups = d_in / 64;
+  const uint32_t row_bytes = (uint32_t)d_in * BITS / 8;
+  const int sets = (d_out + RW - 1) / RW;
+  auto mk = [](const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                             0x00020000);
+  };
+  const auto wr = mk(wq, (uint32_t)((size_t)d_out * row_bytes));
+  const auto sr = mk(scales, (uint32_t)((size_t)d_out * groups * 2));
+  const auto br = mk(biases, (uint32_t)((size_t)d_out * groups * 2));
+  const auto xr = mk(x, (uint32_t)d_in * 2);
+
+  auto load = [&](PersistSet<BITS, RW, UPL>& R, int set) {
+    const bool live = set < sets;  // wave-uniform
+#pragma unroll
+    for (int j = 0; j < UPL; ++j) {
+      const int u = lane + kWave * j;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        const int row = set * RW + r;
+        const bool ok = live && row < d_out && u < units;
+        const uint32_t co = ok ? (uint32_t)row * row_bytes + (uint32_t)u * 16 : kOOR;
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0);
+        R.w[j][r][0] = v.x; R.w[j][r][1] = v.y; R.w[j][r][2] = v.z; R.w[j][r][3] = v.w;
+        const uint32_t so = ok ? ((uint32_t)row * groups + u / kUnitsPerGroup) * 2 : kOOR;
+        R.s[j][r] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
+        R.b[j][r] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+      }
+    }
+  };
+
+  // This lane's activation units (requested before the weights, so their
+  // wait does not hold for the ring), then pair-ordered with their sums.
+  uint32_t nat[UPL][kXW];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = lane + kWave * j;
+    const uint32_t xo = u < units ? (uint32_t)u * G::kUnitCodes * 2 : kOOR;
+#pragma unroll
+    for (int i = 0; i < kXW; i += 4) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 4 * i, 0, 0);
+      nat[j][i] = v.x; nat[j][i + 1] = v.y; nat[j][i + 2] = v.z; nat[j][i + 3] = v.w;
+    }
+  }
+  PersistSet<BITS, RW, UPL> ring[PD];
+#pragma unroll
+  for (int p = 0; p < PD; ++p) load(ring[p], wg + n_waves * p);
+
+  uint32_t xp[UPL][kXW];
+  float xsum[UPL];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kXW; ++i) sum = dot2(nat[j][i], 0x3C003C00u, sum);
+    xsum[j] = sum;
+    constexpr int H = G::kPairsPerWord;
+#pragma unroll
+    for (int wi = 0; wi < G::kUnitWords; ++wi)
+      pair_order<BITS>(&nat[j][wi * (G::kCodesPerWord / 2)], &xp[j][wi * H]);
+  }
+
+  for (int base = wg; base < sets; base += PD * n_waves) {  // wave-uniform
+#pragma unroll
+    for (int p = 0; p < PD; ++p) {
+      const int set = base + p * n_waves;
+      if (set < sets) {  // wave-uniform
+        float acc[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) {
+          float d[RW][1];
+          unit_dot<BITS, 1, RW>(ring[p].w[j], xp[j], G::kSlotPairs, d);
+#pragma unroll
+          for (int r = 0; r < RW; ++r)
+            acc[r] = fmaf(f16_bits_to_f32((uint16_t)ring[p].s[j][r]), d[r][0],
+                          fmaf(f16_bits_to_f32((uint16_t)ring[p].b[j][r]), xsum[j], acc[r]));
+        }
+        load(ring[p], set + PD * n_waves);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const int rs = __builtin_bit_cast(int, row16_sum(acc[r]));
+          const float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(rs, 0)) +
+                          __builtin_bit_cast(float, __builtin_amdgcn_readlane(rs, 16)) +
+                          __builtin_bit_cast(float, __builtin_amdgcn_readlane(rs, 32)) +
+                          __builtin_bit_cast(float, __builtin_amdgcn_readlane(rs, 48));
+          if (lane == r && set * RW + r < d_out) store_out<OutT>(out + set * RW + r, v);
+        }
+      }
+    }
+  }
+}
+
 // Largest LDS footprint the resident path accepts: at least two blocks per CU.
 constexpr size_t kResidentLdsMax = 64 * 1024;
 
@@ -659,6 +779,30 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
   // chunked. KVP_QMV_PATH overrides for tiling sweeps.
   int path = env_int("KVP_QMV_PATH", 0);
   if (path == 0) path = (M == 1) ? 1 : (res_lds <= kResidentLdsMax ? 2 : 3);
+  if constexpr (M == 1 && G::kMagic) {
+    const int upl = (units + kWave - 1) / kWave;
+    // Persistent waves pay off when each has many row sets to walk: very
+    // tall matrices (measured: 151936 x 2560 at 4 bits, 51.5 against 68.7 us).
+    if ((path == 5 || (path == 0 && d_out >= 65536)) && upl <= 4) {
+      int dev = 0, cus = 0;
+      hipGetDevice(&dev);
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      const int sets = (d_out + 1) / 2;
+      int blocks = cus * env_int("KVP_QMV_PER_CU", 2);
+      blocks = min(blocks, (sets + kWavesPerBlock - 1) / kWavesPerBlock);
+#define KVP_PERSIST(U)                                                                         \
+  if (upl <= U) {                                                                              \
+    hipLaunchKernelGGL((qmv_persist_kernel<BITS, 2, U, 4, OutT>), dim3(blocks), dim3(kBlock), 0, \
+                       stream, static_cast<const f16*>(x), wq,                                 \
+                       static_cast<const uint16_t*>(scales),                                   \
+                       static_cast<const uint16_t*>(biases), static_cast<OutT*>(out), d_in,   \
+                       d_out);                                                                 \
+    return check_launch("kvp_qmv");                                                           \
+  }
+      KVP_PERSIST(1) KVP_PERSIST(2) KVP_PERSIST(4)
+#undef KVP_PERSIST
+    }
+  }
   if constexpr (M <= 2) {
     if (path == 1) {
       const int sets = (d_out + RW - 1) / RW;

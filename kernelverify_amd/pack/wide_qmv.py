@@ -44,7 +44,8 @@ def rows_per_wave(m: int) -> int:
     return 2 if m <= 8 else 1
 
 
-KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h", "csrc/qmv_mfma.hip", "csrc/mfma_core.h")
+KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h", "csrc/qmv_mfma.hip", "csrc/mfma_core.h",
+                  "csrc/common.h")
 
 
 def kernel_source_sha256() -> str:
