@@ -60,11 +60,6 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
 
 // DPP lane moves within 16-lane rows (bound_ctrl: lanes without a source
 // read zero), and the row-wide reductions built from them: after four steps
@@ -100,6 +95,15 @@ __device__ __forceinline__ int row16_max_i(int v) {
   v = max(v, dpp_i<kQuadSwap2>(v));
   v = max(v, dpp_i<kHalfMirror>(v));
   return max(v, dpp_i<kRowMirror>(v));
+}
+
+// Max over the 64 lanes, the same value in every lane (as wave_sum).
+__device__ __forceinline__ float wave_max(float v) {
+  const int r = __builtin_bit_cast(int, row16_max(v));
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(r, 48))));
 }
 
 // Sum over the 64 lanes, the same value in every lane: DPP steps within each

@@ -37,17 +37,33 @@ constexpr int kPermuteTile = 8192;  // routed pairs (n * k) one permutation hold
 // ---------------------------------------------------------------------------
 // Routing
 // ---------------------------------------------------------------------------
-// Wave-wide argmax by (value desc, index asc): the winner every lane agrees on.
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(v, off, kWave);
-    const int oi = __shfl_xor(i, off, kWave);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
+// Wave-wide argmax by (value desc, index asc): the winner every lane agrees
+// on. The order is total, so any pairing of lanes reaches it: DPP steps
+// within each 16-lane row, then the four row winners read as scalars.
+__device__ __forceinline__ void take_better(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
   }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  take_better(v, i, dpp_f<CTRL>(v), dpp_i<CTRL>(i));
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  argmax_step<kQuadSwap1>(v, i);
+  argmax_step<kQuadSwap2>(v, i);
+  argmax_step<kHalfMirror>(v, i);
+  argmax_step<kRowMirror>(v, i);
+  const int vb = __builtin_bit_cast(int, v);
+  float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vb, 0));
+  int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+  for (int row = 16; row < kWave; row += 16)
+    take_better(bv, bi, __builtin_bit_cast(float, __builtin_amdgcn_readlane(vb, row)),
+                __builtin_amdgcn_readlane(i, row));
+  v = bv;
+  i = bi;
 }
 
 // logits: E fp32 values of one token, held as E/64 per lane (lane-strided).

@@ -38,11 +38,21 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "6468a849ef55ef35fc29a84fc321ba0b79afc92ac0a1a88b180def73e464dcff"
+RECORDING_SHA256 = "0243b4dad451d03263926f3d76ac2bed5cde2d2b01a070ddda256809668894c5"
 
-KERNEL_SOURCE_SHA256 = "701eba9f3d56faf50625aa3a6e5b8a5e4b46346ad2b1d3e8d4a38c13fe47cea5"
+KERNEL_SOURCE_SHA256 = "501f0001497ec132311628df0dc3da6e3439d2090d69350d8107ba811b405b4e"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
+# ... except 4-bit M = 1 rows of at most 4096 codes over at least 8192 rows,
+# which the library walks four to a wave.
+WIDE_RW_CELLS = frozenset({(4, 1)})  # (bits, m) whose tall short-row shapes use RW = 4
+
+
+def rows_per_wave(m: int, bits: int, d_out: int, d_in: int) -> int:
+    """The pinned launch config of a priced cell."""
+    if (bits, m) in WIDE_RW_CELLS and d_in <= 4096 and d_out >= 8192:
+        return 4
+    return ROWS_PER_WAVE[m]
 
 # Cells measured WIN but not routed, with the reason. A window only admits
 # cells contiguous with its lower part: lm_head 4-bit M = 8 won (the launch
@@ -74,9 +84,10 @@ def _derive(record: dict, kernel_sha: str | None = None) -> tuple[dict, dict]:
     windows: dict[tuple[int, int, int], set] = {}
     for point in record["points"]:
         m, r, bits = point["m"], point["r"], point["bits"]
-        if ROWS_PER_WAVE.get(m) != r:
+        pinned_rw = rows_per_wave(m, bits, point["d_out"], point["d_in"]) if m in ROWS_PER_WAVE else None
+        if pinned_rw != r:
             raise ValueError(f"{point['site']} {bits}-bit M={m} was priced at RW={r}, but the "
-                             f"pinned launch config is RW={ROWS_PER_WAVE.get(m)}")
+                             f"pinned launch config is RW={pinned_rw}")
         shape = (point["d_out"], point["d_in"])
         if shape not in shapes.setdefault(bits, []):
             shapes[bits].append(shape)

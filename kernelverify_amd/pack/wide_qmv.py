@@ -39,8 +39,12 @@ WAVES_PER_BLOCK = 4
 OUT_DTYPES = {"float16": lib.KVP_F16, "float32": lib.KVP_F32}
 
 
-def rows_per_wave(m: int) -> int:
-    """RW: rows a wave walks together (the VGPR budget of M * RW accumulators)."""
+def rows_per_wave(m: int, bits: int = 4, d_out: int = 0, d_in: int = 1 << 30) -> int:
+    """RW: rows a wave of the VALU paths walks together (the VGPR budget of
+    M * RW accumulators). 4-bit M = 1 rows of at most 4096 codes over at
+    least 8192 rows take four (csrc/qmv.hip, launch_qmv_rw)."""
+    if m == 1 and bits == 4 and d_in <= 4096 and d_out >= 8192:
+        return 4
     return 2 if m <= 8 else 1
 
 
@@ -71,9 +75,9 @@ def should_dispatch(m: int, bits: int, d_out: int, d_in: int) -> bool:
     return m in routed_windows.window_for(bits, d_out, d_in)
 
 
-def launch_config(d_out: int, m: int) -> tuple:
+def launch_config(d_out: int, m: int, bits: int = 4, d_in: int = 1 << 30) -> tuple:
     """(grid, block, RW): blocks of four waves over ceil(d_out / (4 * RW))."""
-    r = rows_per_wave(m)
+    r = rows_per_wave(m, bits, d_out, d_in)
     rows_per_block = WAVES_PER_BLOCK * r
     return (((d_out + rows_per_block - 1) // rows_per_block, 1, 1),
             (WAVE * WAVES_PER_BLOCK, 1, 1), r)

@@ -79,7 +79,7 @@ def verify(runner: HipRunner, *, shapes=SHAPES, bits_list=VERIFY_BITS, ms=VERIFY
             rng = np.random.default_rng(11)
             batches, expected = [], []
             for m in ms:
-                grid, block, r = wide_qmv.launch_config(d_out, m)
+                grid, block, r = wide_qmv.launch_config(d_out, m, bits, d_in)
                 subs = {"T": "half", "BITS": bits, "M": m, "R": r}
                 spec_ev = evidence.specialization(wide_qmv.KERNEL_NAME, "quantized_matmul",
                                                   subs, block)

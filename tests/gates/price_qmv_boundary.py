@@ -235,7 +235,7 @@ def price_cell(site, bits, m, d_out, d_in, ours_copies, inc_copies, gemm, stream
     g_ours.destroy()
     g_inc.destroy()
     return classify(a, b, site=site, bits=bits, d_out=d_out, d_in=d_in, m=m,
-                    r=wide_qmv.rows_per_wave(m))
+                    r=wide_qmv.rows_per_wave(m, bits, d_out, d_in))
 
 
 # ---------------------------------------------------------------------------
@@ -335,7 +335,8 @@ def run(sites=SITES, bits_list=BITS, out=print) -> dict:
         "shape_provenance": "six Qwen3-4B decode shapes of the reference's pricing recording "
                             "plus the three BASELINE qmv shapes",
         "kernel_source_sha256": wide_qmv.kernel_source_sha256(),
-        "rows_per_wave": {str(m): wide_qmv.rows_per_wave(m) for m in M_SWEEP},
+        "rows_per_wave": {f"{bits}b {d_out}x{d_in} M{m}": wide_qmv.rows_per_wave(m, bits, d_out, d_in)
+                          for _, d_out, d_in in sites for bits in bits_list for m in M_SWEEP},
         "machine": machine(),
         "elapsed_s": round(time.time() - started, 1),
         "verification": verification,

@@ -22,11 +22,11 @@ from tests.gates.price_qmv_boundary import classify
 # vendor fp16 GEMM with the whole ratio interval above 1 (4- and 8-bit run on
 # the matrix cores from M = 2), less the excluded lm_head island.
 EXPECTED_TABLE = {
-    (2, 1024, 2560): range(1, 4), (2, 2560, 4096): range(1, 4), (2, 2560, 9728): range(1, 9),
-    (2, 4096, 2560): range(1, 3), (2, 4096, 4096): range(1, 4), (2, 4096, 14336): range(1, 9),
+    (2, 1024, 2560): range(1, 5), (2, 2560, 4096): range(1, 5), (2, 2560, 9728): range(1, 9),
+    (2, 4096, 2560): range(1, 4), (2, 4096, 4096): range(1, 5), (2, 4096, 14336): range(1, 9),
     (2, 9728, 2560): range(1, 4), (2, 14336, 4096): range(1, 5), (2, 151936, 2560): range(1, 2),
     (3, 1024, 2560): range(1, 3), (3, 2560, 4096): range(1, 2), (3, 2560, 9728): range(1, 9),
-    (3, 4096, 2560): range(1, 2), (3, 4096, 4096): range(1, 2), (3, 4096, 14336): range(1, 8),
+    (3, 4096, 2560): range(1, 2), (3, 4096, 4096): range(1, 3), (3, 4096, 14336): range(1, 8),
     (3, 9728, 2560): range(1, 2), (3, 14336, 4096): range(1, 3), (3, 151936, 2560): range(1, 2),
     (4, 1024, 2560): range(1, 9), (4, 2560, 4096): range(1, 7), (4, 2560, 9728): range(1, 12),
     (4, 4096, 2560): range(1, 9), (4, 4096, 4096): range(1, 9), (4, 4096, 14336): range(1, 17),
@@ -61,7 +61,11 @@ def test_pins_match_the_live_kernel_and_launch_config():
     """The recording priced these sources at this launch config; an edited
     kernel or a changed RW voids the windows until it is priced again."""
     assert rw.KERNEL_SOURCE_SHA256 == wide_qmv.kernel_source_sha256()
-    assert all(rw.ROWS_PER_WAVE[m] == wide_qmv.rows_per_wave(m) for m in range(1, 17))
+    for bits in (2, 3, 4, 8):
+        for d_out, d_in in ((14336, 4096), (4096, 14336), (4096, 4096), (151936, 2560), (1024, 2560)):
+            for m in range(1, 17):
+                assert rw.rows_per_wave(m, bits, d_out, d_in) == wide_qmv.rows_per_wave(
+                    m, bits, d_out, d_in), (bits, d_out, d_in, m)
 
 
 def test_the_recording_is_read_only_as_its_pinned_bytes(tmp_path):
