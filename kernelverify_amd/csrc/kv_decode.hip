@@ -70,7 +70,8 @@ struct KvArgs {
   const f16* new_k;
   const f16* new_v;
   const int32_t* t_cached;
-  float* part;           // [B][H][n_chunks][2 + DH] per-chunk (m, l, o), m in base-2 units
+  float* part;           // [B][H][n_chunks + 1][2 + DH] per-chunk (m, l, o), m in base-2
+                         // units; slot n_chunks holds the new entry (s_new, 1, new_v)
   void* out;
   int out_f32;
   int n_heads, n_kv_heads, t_stride, chunk, n_chunks, per_seq;
@@ -87,6 +88,31 @@ __device__ __forceinline__ uint32_t load_block8(const uint32_t* __restrict__ row
   return __builtin_amdgcn_alignbit(row[w + 1], row[w], sh);
 }
 
+// The new entry of a block's G query heads as one more partial, slot
+// n_chunks: m = s_new = q . new_k * scale (base 2), l = 1, o = new_v. Chunk 0
+// of every (sequence, KV head) writes it, also for an empty cache, so the
+// combine merges partials only.
+template <int DH, int G>
+__device__ __forceinline__ void write_new_entry(const KvArgs& a, int b, int hk) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const f16* nk = a.new_k + ((size_t)b * a.n_kv_heads + hk) * DH;
+  const f16* nv = a.new_v + ((size_t)b * a.n_kv_heads + hk) * DH;
+  for (int g = wave; g < G; g += kWaves) {  // wave-uniform
+    const int h = hk * G + g;
+    const f16* qh = a.q + ((size_t)b * a.n_heads + h) * DH;
+    float s = 0.0f;
+    for (int d = lane; d < DH; d += kWave) s = fmaf((float)qh[d], (float)nk[d], s);
+    s = wave_sum(s) * a.scale;
+    float* pp =
+        a.part + (((size_t)b * a.n_heads + h) * (a.n_chunks + 1) + a.n_chunks) * partial_floats(DH);
+    for (int d = lane; d < DH; d += kWave) pp[2 + d] = (float)nv[d];
+    if (lane == 0) {
+      pp[0] = s;
+      pp[1] = 1.0f;
+    }
+  }
+}
+
 // Merge of the chunk partials of one query head and the new entry:
 // M = max(m_c, s_new), L = sum l_c 2^(m_c-M) + 2^(s_new-M),
 // out = (sum o_c 2^(m_c-M) + 2^(s_new-M) new_v) / L   (base-2 units).
@@ -101,36 +127,26 @@ constexpr int kCombGroups = kBlock / kCombDims;
 template <int DH, typename OutT>
 __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
   const int z = blockIdx.x;  // b * H + h
-  const int b = z / a.n_heads, h = z - b * a.n_heads;
-  const int hk = h / (a.n_heads / a.n_kv_heads);
+  const int b = z / a.n_heads;
   const int d0 = blockIdx.y * kCombDims;
   const int T = min(max(a.t_cached[b], 0), a.t_stride);  // as the split kernel clamps it
   const int nc = (T + a.chunk - 1) / a.chunk;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  __shared__ float s_new_sh;
   __shared__ float gm[kCombGroups], gl[kCombGroups];
   __shared__ float go[kCombGroups][kCombDims];
 
-  const float* pz = a.part + (size_t)z * a.n_chunks * partial_floats(DH);
+  // Entries 0 .. nc - 1 are the chunks, entry nc the new token (slot n_chunks).
+  const float* pz = a.part + (size_t)z * (a.n_chunks + 1) * partial_floats(DH);
   const int dd = threadIdx.x % kCombDims, grp = threadIdx.x / kCombDims;
   float M = -INFINITY, L = 0.0f, O = 0.0f;
 #pragma unroll 4
-  for (int c = grp; c < nc; c += kCombGroups) {
-    const float* pc = pz + c * partial_floats(DH);
+  for (int c = grp; c <= nc; c += kCombGroups) {
+    const float* pc = pz + (c < nc ? c : a.n_chunks) * partial_floats(DH);
     const float mc = pc[0], lc = pc[1], oc = pc[2 + d0 + dd];
     const float mn = fmaxf(M, mc);
-    const float ea = exp2f(M - mn), eb = exp2f(mc - mn);  // first chunk: ea = 2^-inf = 0
+    const float ea = exp2f(M - mn), eb = exp2f(mc - mn);  // first entry: ea = 2^-inf = 0
     L = fmaf(L, ea, lc * eb);
     O = fmaf(O, ea, oc * eb);
     M = mn;
-  }
-  if (wave == 0) {  // the new entry at full precision: s_new = q . new_k * scale
-    const f16* qh = a.q + (size_t)z * DH;
-    const f16* nk = a.new_k + ((size_t)b * a.n_kv_heads + hk) * DH;
-    float s = 0.0f;
-    for (int d = lane; d < DH; d += kWave) s = fmaf((float)qh[d], (float)nk[d], s);
-    s = wave_sum(s) * a.scale;
-    if (lane == 0) s_new_sh = s;
   }
   go[grp][dd] = O;
   if (dd == 0) {
@@ -139,17 +155,13 @@ __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
   }
   __syncthreads();
   if (threadIdx.x < kCombDims) {
-    const float s_new = s_new_sh;
-    float Mx = s_new;
+    float Mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < kCombGroups; ++i) Mx = fmaxf(Mx, gm[i]);
-    const float e_new = exp2f(s_new - Mx);
-    const f16* nv = a.new_v + ((size_t)b * a.n_kv_heads + hk) * DH;
-    float v = e_new * (float)nv[d0 + dd];
-    float Lx = e_new;
+    float v = 0.0f, Lx = 0.0f;
 #pragma unroll
     for (int i = 0; i < kCombGroups; ++i) {
-      const float e = gl[i] > 0.0f ? exp2f(gm[i] - Mx) : 0.0f;  // groups without chunks
+      const float e = gl[i] > 0.0f ? exp2f(gm[i] - Mx) : 0.0f;  // groups without entries
       v = fmaf(go[i][dd], e, v);
       Lx = fmaf(gl[i], e, Lx);
     }
@@ -183,6 +195,7 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(KvArgs a) {
   // its allocation whatever the caller passes.
   const int T = min(max(a.t_cached[b], 0), a.t_stride);
   const int nc = (T + a.chunk - 1) / a.chunk;
+  if (c == 0) write_new_entry<DH, G>(a, b, blockIdx.y);
   if (c >= nc) return;  // chunk past this sequence: no partial (block-uniform)
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -369,7 +382,7 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(KvArgs a) {
       float v = 0.0f;
 #pragma unroll
       for (int i = 0; i < kWaves; ++i) v += obuf[i][g][dd];
-      float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * a.n_chunks + c) * partial_floats(DH);
+      float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * (a.n_chunks + 1) + c) * partial_floats(DH);
       pp[2 + dd] = v;
       if (dd == 0) {
         pp[0] = stat_m[g];
@@ -610,7 +623,10 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   const int c = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int T = min(max(a.t_cached[b], 0), a.t_stride);
   const int slice0 = c * a.chunk;
-  if (slice0 >= T) return;  // block-uniform
+  if (slice0 >= T) {  // block-uniform
+    if (c == 0) write_new_entry<DH, G>(a, b, hk);
+    return;
+  }
   const int n = min(a.chunk, T - slice0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -637,6 +653,8 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   KvStepRegs<BITS, DH, G> RA, RB;
   auto step_pos = [&](int t) { return t < nsteps ? kP * t : a.chunk + kP; };
   if (wave < nsteps) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
+  // The new entry's partial, while the first cache loads are in flight.
+  if (c == 0) write_new_entry<DH, G>(a, b, hk);
 
   // Query table in LDS (G rows, then a zero row), and qsum_g[h] * scale.
   for (int i = threadIdx.x; i < (G + 1) * (DH / 8); i += kBlock) {
@@ -973,7 +991,7 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
       L = fmaf(wl[w][g], e, L);
       O = fmaf(wo[w][g][dd], e, O);
     }
-    float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * a.n_chunks + c) * partial_floats(DH);
+    float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * (a.n_chunks + 1) + c) * partial_floats(DH);
     pp[2 + dd] = O;
     if (dd == 0) {
       pp[0] = M;
@@ -1002,7 +1020,7 @@ int pick_chunk(int bits, int batch, int n_kv_heads, int t_stride, int G) {
 
 template <int BITS, int DH, int G>
 int launch_dh_g(const KvArgs& a, int batch, hipStream_t st) {
-  if (a.t_stride > 0) {
+  {  // also for an empty cache: chunk 0 writes the new entry
     const dim3 grid(a.n_chunks, a.n_kv_heads, batch);
     if constexpr ((BITS == 4 || BITS == 8) && G <= 8) {
       hipLaunchKernelGGL((kv_mfma_split_kernel<BITS, DH, G>), grid, dim3(kBlock), 0, st, a);
@@ -1049,7 +1067,7 @@ extern "C" size_t kvp_kv_decode_workspace_bytes(int batch, int n_heads, int head
   if (batch < 1 || n_heads < 1 || head_dim < 1 || t_stride < 0) return 0;
   if (chunk <= 0) chunk = 64;  // the smallest chunk the library picks
   const size_t n_chunks = t_stride > 0 ? (t_stride + chunk - 1) / chunk : 1;
-  return (size_t)batch * n_heads * n_chunks * kvp::partial_floats(head_dim) * sizeof(float);
+  return (size_t)batch * n_heads * (n_chunks + 1) * kvp::partial_floats(head_dim) * sizeof(float);
 }
 
 extern "C" int kvp_kv_decode(const void* q, const uint32_t* k_wq, const void* k_scales,

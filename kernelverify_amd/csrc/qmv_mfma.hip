@@ -258,10 +258,16 @@ int launch_mt(const void* x, const uint32_t* wq, const void* s, const void* b, v
 template <int BITS, int MT, typename OutT>
 int launch_tiles(const void* x, const uint32_t* wq, const void* s, const void* b, void* out,
                  int m, int d_out, int d_in, hipStream_t st) {
-  // Two tiles per block halve the x staging per weight byte; with few tiles
-  // one tile per block and eight waves on it keep enough loads in flight.
+  // More tiles per block share one x staging (less staging per weight
+  // byte) but leave fewer blocks. Measured on MI355X: four tiles for 768 to
+  // 4095 tiles (and from 512 at M >= 8), two for taller matrices at M >= 8,
+  // else one tile with eight waves on it to keep loads in flight.
   const int tiles = (d_out + 15) / 16;
-  const int v = env_int("KVP_QMV_MFMA_TILES", (tiles >= 768 && (tiles < 4096 || m >= 8)) ? 2 : 1);
+  int pick = 1;
+  if (tiles < 4096 && (tiles >= 768 || (tiles >= 512 && m >= 8))) pick = 4;
+  else if (tiles >= 4096 && m >= 8) pick = 2;
+  const int v = env_int("KVP_QMV_MFMA_TILES", pick);
+  if (v == 4) return launch_mt<BITS, MT, 4, 4, OutT>(x, wq, s, b, out, m, d_out, d_in, st);
   if (v == 2) return launch_mt<BITS, MT, 2, 4, OutT>(x, wq, s, b, out, m, d_out, d_in, st);
   if (tiles >= 512) return launch_mt<BITS, MT, 1, 4, OutT>(x, wq, s, b, out, m, d_out, d_in, st);
   return launch_mt<BITS, MT, 1, 8, OutT>(x, wq, s, b, out, m, d_out, d_in, st);
