@@ -38,9 +38,9 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "0243b4dad451d03263926f3d76ac2bed5cde2d2b01a070ddda256809668894c5"
+RECORDING_SHA256 = "7b2caf8f8024052c03ffcf99247649d2ee608b5593d3989dfe5dc44a461708ad"
 
-KERNEL_SOURCE_SHA256 = "501f0001497ec132311628df0dc3da6e3439d2090d69350d8107ba811b405b4e"
+KERNEL_SOURCE_SHA256 = "0313dc8bad44181876d188c25bea6495fc8dc685a5df18e1de9f7a33023d8643"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
 # ... except 4-bit M = 1 rows of at most 4096 codes over at least 8192 rows,
@@ -55,10 +55,11 @@ def rows_per_wave(m: int, bits: int, d_out: int, d_in: int) -> int:
     return ROWS_PER_WAVE[m]
 
 # Cells measured WIN but not routed, with the reason. A window only admits
-# cells contiguous with its lower part: lm_head 4-bit M = 8 won (the launch
-# switches to two row tiles per block from M = 8 at this height) above a
-# REFUSED M = 6 and a LOSS at M = 7, so it is an island, not a window edge.
-EXCLUDED_CELLS = MappingProxyType({(4, 151936, 2560): frozenset({8})})
+# cells contiguous with its lower part; these won at M = 8, where the launch
+# switches to more row tiles per block, above measured losses at M = 6-7
+# (lm_head 4-bit) and M = 5-7 (gate/up 8-bit): islands, not window edges.
+EXCLUDED_CELLS = MappingProxyType({(4, 151936, 2560): frozenset({8}),
+                                   (8, 9728, 2560): frozenset({8})})
 
 
 def _load(path: Path = RECORDING_PATH, pinned: str | None = None) -> dict:
