@@ -652,17 +652,57 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   // of the buffers' range, it reads zeros without traffic.
   KvStepRegs<BITS, DH, G> RA, RB;
   auto step_pos = [&](int t) { return t < nsteps ? kP * t : a.chunk + kP; };
+  // The small inputs go out before the first cache loads, so (returns being
+  // in order) they are in registers while the cache is still in flight: the
+  // query table (G rows, then a zero row; at most one 16-byte item per
+  // thread) and, in chunk 0, the new entry's q . new_k operands and new_v.
+  static_assert((G + 1) * (DH / 8) <= kBlock, "one query-table item per thread");
+  const int qi_row = threadIdx.x / (DH / 8), qi_c8 = threadIdx.x % (DH / 8);
+  u32x4 qv = {0, 0, 0, 0};
+  if (qi_row < G)
+    qv = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + qi_row) * DH +
+                                         8 * qi_c8);
+  constexpr int kNE = (G + kWaves - 1) / kWaves, kND = DH / kWave;  // heads per wave, dims per lane
+  float ne_q[kNE][kND], ne_k[kNE][kND], ne_v[kNE][kND];
+  if (c == 0) {
+#pragma unroll
+    for (int e = 0; e < kNE; ++e) {
+      const int g = min(wave + kWaves * e, G - 1);
+      const f16* qh = a.q + ((size_t)b * a.n_heads + h0 + g) * DH;
+      const f16* nk = a.new_k + ((size_t)b * a.n_kv_heads + hk) * DH;
+      const f16* nv = a.new_v + ((size_t)b * a.n_kv_heads + hk) * DH;
+#pragma unroll
+      for (int i = 0; i < kND; ++i) {
+        ne_q[e][i] = (float)qh[lane + kWave * i];
+        ne_k[e][i] = (float)nk[lane + kWave * i];
+        ne_v[e][i] = (float)nv[lane + kWave * i];
+      }
+    }
+  }
   if (wave < nsteps) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
-  // The new entry's partial, while the first cache loads are in flight.
-  if (c == 0) write_new_entry<DH, G>(a, b, hk);
 
-  // Query table in LDS (G rows, then a zero row), and qsum_g[h] * scale.
-  for (int i = threadIdx.x; i < (G + 1) * (DH / 8); i += kBlock) {
-    const int row = i / (DH / 8), c8 = i % (DH / 8);
-    u32x4 v = {0, 0, 0, 0};
-    if (row < G)
-      v = *reinterpret_cast<const u32x4*>(a.q + ((size_t)b * a.n_heads + h0 + row) * DH + 8 * c8);
-    *reinterpret_cast<u32x4*>(&qtab[row * DH + 8 * c8]) = v;
+  if (qi_row <= G) *reinterpret_cast<u32x4*>(&qtab[qi_row * DH + 8 * qi_c8]) = qv;
+  // The new entry's partial (slot n_chunks: m = q . new_k * scale, l = 1,
+  // o = new_v), while the first cache loads are in flight.
+  if (c == 0) {
+#pragma unroll
+    for (int e = 0; e < kNE; ++e) {
+      const int g = wave + kWaves * e;
+      if (g < G) {  // wave-uniform
+        float sdot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kND; ++i) sdot = fmaf(ne_q[e][i], ne_k[e][i], sdot);
+        sdot = wave_sum(sdot) * a.scale;
+        float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * (a.n_chunks + 1) + a.n_chunks) *
+                                 partial_floats(DH);
+#pragma unroll
+        for (int i = 0; i < kND; ++i) pp[2 + lane + kWave * i] = ne_v[e][i];
+        if (lane == 0) {
+          pp[0] = sdot;
+          pp[1] = 1.0f;
+        }
+      }
+    }
   }
   __syncthreads();
   {
@@ -1008,10 +1048,12 @@ int pick_chunk(int bits, int batch, int n_kv_heads, int t_stride, int G) {
   // fixed set-up and merge: about one block per CU (256 over the longest
   // sequence) measured best. The register-prefetched kernel holds its whole
   // chunk (128 positions at most): about 1024 blocks.
-  // Several sequences of mixed lengths balance better over smaller slices
-  // (measured: 8 sequences up to 32k, 512 beats 1024).
+  // Several sequences of mixed lengths leave many slices empty (the host
+  // sizes by t_stride, not by the lengths on the device), so they take
+  // longer slices (measured, 8 sequences of 1k-32k: 4096 beats 2048 by 10%,
+  // 512 by 25%).
   const bool mfma = use_mfma(bits, G);
-  const int cap = mfma ? (batch > 1 ? 512 : 1024) : 128;
+  const int cap = mfma ? (batch > 1 ? 4096 : 1024) : 128;
   const long target = (long)batch * n_kv_heads * t_stride / (mfma ? 256 : 1024);
   int chunk = 64;
   while (chunk < cap && chunk < target) chunk *= 2;

@@ -46,10 +46,14 @@ def uses_matrix_cores(bits: int, gqa: int) -> bool:
     return bits in (4, 8) and gqa <= 8
 
 
-def max_chunk(bits: int, gqa: int = 4) -> int:
-    """Largest chunk (positions per block): the MFMA kernel walks its slice
-    tile by tile; the VALU kernel holds its chunk's codes in registers."""
-    return 1024 if uses_matrix_cores(bits, gqa) else 128
+def max_chunk(bits: int, gqa: int = 4, batch: int = 1) -> int:
+    """Largest chunk the library picks (positions per block): the MFMA
+    kernel walks its slice tile by tile, longer slices for several sequences
+    (whose lengths the host does not know); the VALU kernel holds its
+    chunk's codes in registers. Mirrors ``pick_chunk`` in csrc/kv_decode.hip."""
+    if uses_matrix_cores(bits, gqa):
+        return 4096 if batch > 1 else 1024
+    return 128
 
 
 def launch_config(batch: int, n_kv_heads: int, t_stride: int, bits: int = 4,
@@ -60,7 +64,7 @@ def launch_config(batch: int, n_kv_heads: int, t_stride: int, bits: int = 4,
     if not chunk:
         target = batch * n_kv_heads * t_stride // (256 if uses_matrix_cores(bits, gqa) else 1024)
         chunk = 64
-        while chunk < max_chunk(bits, gqa) and chunk < target:
+        while chunk < max_chunk(bits, gqa, batch) and chunk < target:
             chunk *= 2
     n_chunks = max(1, -(-t_stride // chunk))
     return (n_chunks, n_kv_heads, batch), (256, 1, 1), chunk
