@@ -775,10 +775,17 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
   const int units = d_in / G::kUnitCodes;
   const size_t res_lds = resident_lds_bytes<BITS, M>(d_in);
   // Path: 1 streaming (no LDS; M <= 2), 2 resident x, 3 chunked x. Auto
-  // (measured on MI355X): streaming for M = 1, resident when x fits, else
-  // chunked. KVP_QMV_PATH overrides for tiling sweeps.
+  // (measured on MI355X): streaming for M = 1 except tall 4-bit matrices of
+  // short rows (below), resident when x fits, else chunked. KVP_QMV_PATH
+  // overrides for tiling sweeps.
+  // Tall 4-bit M = 1 with rows of at most 4096 codes: x resident in LDS at
+  // four blocks per CU (an equal share on every CU; 3.5 or 6 per CU lose),
+  // two rows per wave. Measured against streaming: 14336 x 4096 8.46 / 8.85
+  // us, 9728 x 2560 6.07 / 6.88, 8192 x 4096 6.15 / 6.41; 4096 x 4096 stays
+  // streaming (5.07 / 4.47).
+  const bool tall = M == 1 && BITS == 4 && d_in <= 4096 && d_out >= 8192;
   int path = env_int("KVP_QMV_PATH", 0);
-  if (path == 0) path = (M == 1) ? 1 : (res_lds <= kResidentLdsMax ? 2 : 3);
+  if (path == 0) path = (M == 1 && !tall) ? 1 : (res_lds <= kResidentLdsMax ? 2 : 3);
   if constexpr (M == 1 && G::kMagic) {
     const int upl = (units + kWave - 1) / kWave;
     // Persistent waves pay off when each has many row sets to walk: very
@@ -833,6 +840,12 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
     }
     const int sets = (d_out + RW - 1) / RW;
     int blocks = min(cached_blocks, (sets + kWavesPerBlock - 1) / kWavesPerBlock);
+    if (tall) {
+      int dev = 0, cus = 0;
+      hipGetDevice(&dev);
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      blocks = min(blocks, 4 * cus);
+    }
     blocks = env_int("KVP_QMV_BLOCKS", blocks);
     if (blocks < 1) return set_error(KVP_INVALID, "kvp_qmv: KVP_QMV_BLOCKS=%d", blocks);
     hipLaunchKernelGGL((qmv_resident_kernel<BITS, M, RW, OutT>), dim3(blocks), dim3(kBlock),
@@ -872,11 +885,10 @@ template <int BITS, int M, typename OutT>
 int launch_qmv_rw(const void* x, const uint32_t* wq, const void* scales, const void* biases,
                   void* out, int d_out, int d_in, hipStream_t stream) {
   if constexpr (M <= 2) {
-    // Four rows per wave halve the activation work per row; measured faster
-    // for 4-bit M = 1 rows of at most 4096 codes over at least 8192 rows
-    // (14336 x 4096: 8.90 against 9.39 us), slower elsewhere.
-    const int rw_default = (M == 1 && BITS == 4 && d_in <= 4096 && d_out >= 8192) ? 4 : 2;
-    if (env_int("KVP_QMV_RW", rw_default) == 4)
+    // Two rows per wave; four (KVP_QMV_RW=4) halve the activation work per
+    // row of the streaming kernel, which measured faster only where the
+    // resident kernel now serves (tall 4-bit M = 1 rows of <= 4096 codes).
+    if (env_int("KVP_QMV_RW", 2) == 4)
       return launch_qmv<BITS, M, 4, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
     return launch_qmv<BITS, M, 2, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
   } else {

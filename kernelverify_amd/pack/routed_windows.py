@@ -38,20 +38,15 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "7b2caf8f8024052c03ffcf99247649d2ee608b5593d3989dfe5dc44a461708ad"
+RECORDING_SHA256 = "eb04bc55fe54bccff95e7f7c81aaefb00614d998f85b0ae2dc56cfeaa70f6cfa"
 
-KERNEL_SOURCE_SHA256 = "0313dc8bad44181876d188c25bea6495fc8dc685a5df18e1de9f7a33023d8643"
+KERNEL_SOURCE_SHA256 = "c51b09e4f8373e9a494d480835e451273cbc39536dffabf83a25d13d6a504117"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
-# ... except 4-bit M = 1 rows of at most 4096 codes over at least 8192 rows,
-# which the library walks four to a wave.
-WIDE_RW_CELLS = frozenset({(4, 1)})  # (bits, m) whose tall short-row shapes use RW = 4
 
 
 def rows_per_wave(m: int, bits: int, d_out: int, d_in: int) -> int:
     """The pinned launch config of a priced cell."""
-    if (bits, m) in WIDE_RW_CELLS and d_in <= 4096 and d_out >= 8192:
-        return 4
     return ROWS_PER_WAVE[m]
 
 # Cells measured WIN but not routed, with the reason. A window only admits

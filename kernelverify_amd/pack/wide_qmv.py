@@ -41,10 +41,8 @@ OUT_DTYPES = {"float16": lib.KVP_F16, "float32": lib.KVP_F32}
 
 def rows_per_wave(m: int, bits: int = 4, d_out: int = 0, d_in: int = 1 << 30) -> int:
     """RW: rows a wave of the VALU paths walks together (the VGPR budget of
-    M * RW accumulators). 4-bit M = 1 rows of at most 4096 codes over at
-    least 8192 rows take four (csrc/qmv.hip, launch_qmv_rw)."""
-    if m == 1 and bits == 4 and d_in <= 4096 and d_out >= 8192:
-        return 4
+    M * RW accumulators; csrc/qmv.hip, launch_qmv_rw). The same at every
+    shape; the shape arguments stay for callers that pin a priced cell."""
     return 2 if m <= 8 else 1
 
 

@@ -24,7 +24,7 @@ from tests.gates.price_qmv_boundary import classify
 EXPECTED_TABLE = {
     (2, 1024, 2560): range(1, 5), (2, 2560, 4096): range(1, 5), (2, 2560, 9728): range(1, 9),
     (2, 4096, 2560): range(1, 4), (2, 4096, 4096): range(1, 5), (2, 4096, 14336): range(1, 9),
-    (2, 9728, 2560): range(1, 4), (2, 14336, 4096): range(1, 5), (2, 151936, 2560): range(1, 2),
+    (2, 9728, 2560): range(1, 4), (2, 14336, 4096): range(1, 5), (2, 151936, 2560): range(1, 3),
     (3, 1024, 2560): range(1, 3), (3, 2560, 4096): range(1, 2), (3, 2560, 9728): range(1, 9),
     (3, 4096, 2560): range(1, 2), (3, 4096, 4096): range(1, 3), (3, 4096, 14336): range(1, 8),
     (3, 9728, 2560): range(1, 2), (3, 14336, 4096): range(1, 3), (3, 151936, 2560): range(1, 2),
