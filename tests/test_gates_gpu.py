@@ -44,3 +44,23 @@ def test_each_quantizer_fault_turns_the_qmv_gate_red(fault):
                               ms=[1], artefact_fault=FAULTS[fault], out=quiet)
     assert ev.cases_run == 2
     assert ev.cases_passed == 0, (fault, [c for s in ev.specializations for c in s.cases])
+
+
+def test_a_green_gate_certifies_and_a_faulted_one_is_refused(tmp_path):
+    """Certificates from real gate evidence: one per specialization when the
+    gate is green; the family withheld when the artefact is faulted."""
+    import json
+
+    from tests.gates import emit_pack_certificates as emitter
+
+    runner = HipRunner(repeats=1)
+    ev = pack_wide_qmv.verify(runner, shapes=[(512, 1024)], bits_list=(4,), ms=[1, 4],
+                              out=quiet)
+    report = emitter.certify([ev], tmp_path / "green", commit="test", chip="gfx950")
+    assert report.ok and len(report.written) == 2, report.refused
+    body = json.loads(report.written[0].read_text())
+    assert body["protocol_bound"]["cases_passed"] == body["protocol_bound"]["cases_run"] == 2
+    bad = pack_wide_qmv.verify(runner, shapes=[(512, 1024)], bits_list=(4,), ms=[1],
+                               artefact_fault=FAULTS[sorted(FAULTS)[0]], out=quiet)
+    refused = emitter.certify([bad], tmp_path / "faulted", commit="test", chip="gfx950")
+    assert not refused.written and "kvp_qmv" in refused.refused
