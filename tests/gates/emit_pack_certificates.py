@@ -318,7 +318,9 @@ def main(argv=None) -> int:
         commit = proc.stdout.strip() or "unknown"
     runner = HipRunner()
     device = runner.probe()
-    chip = f"{device.name} ({device.arch})" if device is not None else "unknown"
+    chip = "unknown"
+    if device is not None:
+        chip = f"{device.name} ({device.arch})" if device.name.strip() else device.arch
     report = certify(gate_evidence(runner), args.out, commit, chip)
     print(f"written: {len(report.written)} certificate(s) -> {args.out}", flush=True)
     for family, reasons in sorted(report.refused.items()):
