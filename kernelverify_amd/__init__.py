@@ -11,6 +11,9 @@ the host side:
 - ``kernelverify_amd.lib``      ctypes binding of libkvpack.so
 - ``kernelverify_amd.hip``      ctypes binding of the HIP runtime
 - ``kernelverify_amd.build``    hipcc build of libkvpack.so
+- ``kernelverify_amd.report``   verification certificates (schema v2)
+- ``kernelverify_amd.serving``  the PyTorch-ROCm serving door (routed
+                                linear with the flattened-M rule, KV door)
 
 There is no CPU implementation of any operator here: without the built
 library and a gfx950 device every compute call raises.
