@@ -14,6 +14,8 @@ the host side:
 - ``kernelverify_amd.report``   verification certificates (schema v2)
 - ``kernelverify_amd.serving``  the PyTorch-ROCm serving door (routed
                                 linear with the flattened-M rule, KV door)
+- ``kernelverify_amd.checkpoint`` MLX-affine safetensors checkpoints read
+                                without repacking
 
 There is no CPU implementation of any operator here: without the built
 library and a gfx950 device every compute call raises.

@@ -88,3 +88,21 @@ def test_kv_door_reads_the_logical_length_not_the_stride(bits, dh, gqa):
     ref = kv_reference_gqa(q, k_raw, v_raw, nk, nv, bits)
     err = np.max(np.abs(out.reshape(1, h, dh).cpu().numpy().astype(np.float64) - ref))
     assert err <= 4 * 9.77e-4 * np.max(np.abs(ref)), err
+
+
+def test_a_loaded_checkpoint_serves_through_the_patch(tmp_path):
+    """MLX-affine safetensors straight to the device and through the routed
+    linear: the same output as the pack API on the file's own bytes."""
+    from kernelverify_amd.checkpoint import load_quantized_linears, save_quantized_linears
+
+    _, words, art = _layer(4096, 4096, 4, seed=5)
+    save_quantized_linears(tmp_path / "model.safetensors",
+                           {"mlp.up_proj": (words, art.scales, art.biases)}, bits=4)
+    layers = load_quantized_linears(tmp_path)
+    model = nn.Sequential(layers["mlp.up_proj"])
+    patch = Patch(model)
+    x = np.random.default_rng(6).standard_normal((1, 4096)).astype(np.float16)
+    got = model(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    assert patch.calls == 1
+    assert np.array_equal(got.cpu().numpy(), wide_qmv.qmv(x, words, art.scales, art.biases, bits=4))
