@@ -1,0 +1,27 @@
+"""The qmv mutation battery's host side: every mutant differs from the
+control by its own fault and compiles for gfx950 (hiprtc, no device). The
+scoring on the GPU is tests/test_gates_gpu.py."""
+
+import pytest
+
+from kernelverify_amd.runners import rtc
+from tests.gates import battery_qmv as B
+
+
+def test_each_mutant_is_the_control_plus_one_fault():
+    control = B.mutant_spec("control", 4).source
+    sources = {name: B.mutant_spec(name, 4).source for name in B.MUTANTS}
+    assert len(set(sources.values())) == len(B.MUTANTS)
+    for name, src in sources.items():
+        assert src.endswith(B.TEMPLATE) and (name == "control") == (src == control)
+
+
+@pytest.mark.parametrize("name", sorted(B.MUTANTS))
+def test_every_mutant_compiles_for_gfx950(name):
+    try:
+        code = rtc.compile_source(B.mutant_spec(name, 8).source)
+    except rtc.CompileError as error:
+        if "not loadable" in str(error):
+            pytest.skip(str(error))
+        raise
+    assert len(code) > 0

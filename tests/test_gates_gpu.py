@@ -64,3 +64,18 @@ def test_a_green_gate_certifies_and_a_faulted_one_is_refused(tmp_path):
                                artefact_fault=FAULTS[sorted(FAULTS)[0]], out=quiet)
     refused = emitter.certify([bad], tmp_path / "faulted", commit="test", chip="gfx950")
     assert not refused.written and "kvp_qmv" in refused.refused
+
+
+def test_mutation_battery_catches_every_blatant_fault():
+    """The qmv gate's cases against run-time compiled mutants: the control
+    passes and every fault of the operator's formula is caught; the fp16
+    rounding of group partials is reported either way (a precision fault
+    the cases may not separate)."""
+    from tests.gates import battery_qmv
+
+    table = battery_qmv.run_battery(HipRunner(repeats=1))
+    assert not table["control"]["caught"], table["control"]
+    for name in ("fp16-accumulate", "drop-bias", "wrong-group-scale", "complemented-codes",
+                 "shifted-activations"):
+        assert table[name]["caught"], (name, table[name])
+    print({n: (r["caught"], round(r["worst_err_over_tol"], 3)) for n, r in table.items()})
