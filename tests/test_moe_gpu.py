@@ -237,3 +237,13 @@ def test_swiglu_group_count_off_the_matrix_core_tiling():
     out = run_swiglu(x, mats, idx, gate, 4)
     v = judge_swiglu(x, mats, idx, gate, out, None)
     assert v.ok, v
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+def test_one_token_at_every_width(bits):
+    """n = 1 (the decode step of one sequence) at every width, fp32 out."""
+    x, mats, logits = swiglu_case(1, 16, 512, 256, bits, seed=60 + bits)
+    idx, gate = route_topk(logits, 4)
+    out = run_swiglu(x, mats, idx, gate, bits, "float32")
+    v = judge_swiglu(x, mats, idx, gate, out, None, "float32")
+    assert v.ok, (bits, v)
