@@ -851,9 +851,14 @@ int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f3
     if (G % 4 == 0 && G <= 64 && getenv("KVP_MOE_VALU") == nullptr) {
       const size_t lds = ((size_t)kEMT * (G * kEGroupSlots + 1) + 8) * 16 + (size_t)G * kEMT * 8;
       const int tiles = (a.d_out + 15) / 16;
-      // Short rows (at most 4 steps of 4 groups per tile): one
-      // wave per tile, four tiles per block; longer rows: four waves per tile.
-      const bool short_rows = G / 4 <= 4;
+      // One wave per tile and four tiles per block for short rows (at most
+      // 4 steps of 4 groups per tile) and whenever many experts are active
+      // (their x staging then spreads over four tiles; 2048-code rows,
+      // measured: n = 8 61.2 against 62.0 us, n = 32 114.3 against 118.0);
+      // four waves per tile for long rows of a few experts (n = 1: 27.4
+      // against 32.2 us). KVP_MOE_KQ (1 or 4) overrides for tiling sweeps.
+      const char* kq_env = getenv("KVP_MOE_KQ");
+      const bool short_rows = kq_env ? atoi(kq_env) == 1 : (G / 4 <= 4 || max_active >= 32);
       const dim3 grid(short_rows ? (tiles + 3) / 4 : tiles, max_active);
 #define KVP_EXPERT(SW, F32, KQ)                                                               \
   hipLaunchKernelGGL((expert_mfma_kernel<BITS, SW, F32, KQ>), grid, dim3(kBlock), lds, st, a)
