@@ -25,3 +25,25 @@ def test_every_mutant_compiles_for_gfx950(name):
             pytest.skip(str(error))
         raise
     assert len(code) > 0
+
+
+def test_each_kv_mutant_is_the_control_plus_one_fault():
+    from tests.gates import battery_kv as K
+
+    sources = {name: K.mutant_spec(name, 4, 128).source for name in K.MUTANTS}
+    assert len(set(sources.values())) == len(K.MUTANTS)
+    for src in sources.values():
+        assert src.endswith(K.TEMPLATE)
+
+
+@pytest.mark.parametrize("name", ["control", "new-entry-dropped", "fp16-scores", "gqa-modulo"])
+def test_kv_mutants_compile_for_gfx950(name):
+    from tests.gates import battery_kv as K
+
+    try:
+        code = rtc.compile_source(K.mutant_spec(name, 3, 128).source)
+    except rtc.CompileError as error:
+        if "not loadable" in str(error):
+            pytest.skip(str(error))
+        raise
+    assert len(code) > 0

@@ -79,3 +79,18 @@ def test_mutation_battery_catches_every_blatant_fault():
                  "shifted-activations"):
         assert table[name]["caught"], (name, table[name])
     print({n: (r["caught"], round(r["worst_err_over_tol"], 3)) for n, r in table.items()})
+
+
+def test_kv_mutation_battery():
+    """The KV gate's cases against run-time compiled mutants: the control
+    passes, every fault of the formula is caught; the unshifted softmax (C4)
+    and a wrong GQA mapping escape these cases, as the battery documents."""
+    from tests.gates import battery_kv
+
+    table = battery_kv.run_battery(HipRunner(repeats=1))
+    print({n: (r["caught"], round(r["worst_err_over_tol"], 3)) for n, r in table.items()})
+    assert not table["control"]["caught"], table["control"]
+    for name in ("new-entry-dropped", "v-bias-dropped", "v-position-shifted", "scale-1-over-dh"):
+        assert table[name]["caught"], (name, table[name])
+    for name in ("no-max-shift", "gqa-modulo"):
+        assert not table[name]["caught"], (name, table[name])
