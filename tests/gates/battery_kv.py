@@ -9,8 +9,7 @@ the control has none and must pass. CAUGHT means at least one case's error
 exceeds the kv_attention contract tolerance. An escaped mutant is a fault
 these cases cannot see, reported, not hidden: the gate's inputs are small
 enough that an unshifted softmax never overflows (clause C4 is therefore
-attested from source), and its cases all have one query head per KV head,
-so a wrong GQA mapping is invisible to it (tests/test_kv_gpu.py covers GQA).
+attested from source).
 
     python -m tests.gates.battery_kv       # prints the table; exit 1 if the control fails
 """
@@ -30,9 +29,15 @@ from kernelverify_amd.runners import (
     LaunchSpec,
     RunCase,
 )
-from oracle.inputs import kv_case
-from oracle.verify import kv_inputs, reference_and_tolerance
-from tests.gates.pack_kv_attention import EXTRA, VERIFY_BITS, VERIFY_SHAPES, quantize_cache_oracle
+from oracle.verify import reference_and_tolerance
+from tests.gates.pack_kv_attention import (
+    EXTRA,
+    GQA,
+    VERIFY_BITS,
+    VERIFY_SHAPES,
+    case_arrays,
+    quantize_cache_oracle,
+)
 
 MAX_T = 2048
 
@@ -156,21 +161,23 @@ def mutant_spec(name: str, bits: int, dh: int) -> KernelSpec:
 
 def cases():
     """The KV gate's plan (same shapes, widths and seeds), grouped by (bits, DH)."""
-    plan = [(s, bits) for s in VERIFY_SHAPES for bits in VERIFY_BITS] + EXTRA
+    plan = [(s, bits) for s in VERIFY_SHAPES for bits in VERIFY_BITS] + EXTRA + GQA
     grouped: dict = {}
-    for (b, h, t, dh), bits in plan:
+    for shape, bits in plan:
+        b, h, t, dh = shape[:4]
+        hkv = shape[4] if len(shape) > 4 else h
         assert t <= MAX_T
-        q, kc, vc, nk, nv = kv_case(b, h, t, dh, seed=t + bits)
+        (q, kc, vc, nk, nv), judged = case_arrays(b, h, t, dh, bits, hkv)
         k_parts, v_parts = quantize_cache_oracle(kc, bits), quantize_cache_oracle(vc, bits)
-        ref, tol = reference_and_tolerance("kv_attention", kv_inputs(q, kc, vc, nk, nv, bits))
+        ref, tol = reference_and_tolerance("kv_attention", judged)
         case = RunCase(inputs={"q": q, "k_wq": k_parts[0], "k_scales": k_parts[1],
                                "k_biases": k_parts[2], "v_wq": v_parts[0],
                                "v_scales": v_parts[1], "v_biases": v_parts[2],
                                "new_k": nk, "new_v": nv},
-                       params={"b_rows": b, "n_heads": h, "t_cached": t, "n_kv_heads": h,
+                       params={"b_rows": b, "n_heads": h, "t_cached": t, "n_kv_heads": hkv,
                                "t_stride": t},
                        output_shapes=[((b, h, dh), "float16")],
-                       label=f"B={b} H={h} T={t} DH={dh} {bits}-bit")
+                       label=f"B={b} H={h} T={t} DH={dh} HKV={hkv} {bits}-bit")
         grouped.setdefault((bits, dh), []).append((case, ref, tol))
     return grouped
 

@@ -29,10 +29,13 @@ from oracle.verify import judge_case, kv_inputs, reference_and_tolerance
 VERIFY_SHAPES = [(1, 8, 512, 128), (4, 2, 64, 64), (1, 4, 300, 128)]
 VERIFY_BITS = (4, 8)
 EXTRA = [((1, 4, 2048, 128), 4), ((1, 4, 256, 64), 2), ((1, 4, 256, 128), 3)]
+# (B, H, T, DH, HKV): grouped-query cases, H / HKV query heads per cache head
+GQA = [((1, 8, 256, 128, 2), 4)]
 
 GATE_POLICY = (
     "pack-gate fixed-case sweep: 3 fixed (B, H, T, DH) shapes x bits {4, 8}, plus T = 2048 "
-    "(past the reference's 1024 capacity) at 4 bits and one case each at 2 and 3 bits, "
+    "(past the reference's 1024 capacity) at 4 bits, one case each at 2 and 3 bits and one "
+    "grouped-query case (8 query heads over 2 cache heads, judged on the tiled caches), "
     "judged against the oracle's kv_attention reference and ensemble-floor tolerance; GPU "
     "quantizer cache bytes checked identical to the canonical quantizer per case."
 )
@@ -56,21 +59,37 @@ def gpu_cache_identical(cache: np.ndarray, bits: int, parts) -> bool:
     return all(np.array_equal(g.reshape(p.shape), p) for g, p in zip(got, parts))
 
 
+def case_arrays(b, h, t, dh, bits, hkv=None):
+    """(q, k cache, v cache, new_k, new_v) the kernel reads, and the kv_inputs the
+    oracle judges by: a grouped-query case's caches and new entries hold HKV
+    heads, and the oracle reads them tiled to H heads (query head h reads
+    cache head h // (H / HKV); tests/test_oracle_kv_gqa.py pins the tiling)."""
+    q, kc, vc, nk, nv = kv_case(b, h, t, dh, seed=t + bits)
+    hkv = hkv or h
+    kc, vc, nk, nv = kc[:hkv], vc[:hkv], nk[:, :hkv], nv[:, :hkv]
+    r = h // hkv
+    judged = kv_inputs(q, np.repeat(kc, r, axis=0), np.repeat(vc, r, axis=0),
+                       np.repeat(nk, r, axis=1), np.repeat(nv, r, axis=1), bits)
+    return (q, kc, vc, nk, nv), judged
+
+
 def verify(runner: HipRunner, *, cases=None, out=print) -> GateEvidence:
     evidence = GateEvidence(gate="pack_kv_attention", policy=GATE_POLICY,
                             seed_protocol=SEED_PROTOCOL)
     template = kv_attention.kernel_spec()
     plan = cases if cases is not None else (
-        [(s, bits) for s in VERIFY_SHAPES for bits in VERIFY_BITS] + EXTRA)
+        [(s, bits) for s in VERIFY_SHAPES for bits in VERIFY_BITS] + EXTRA + GQA)
     grouped: dict = {}
-    for (b, h, t, dh), bits in plan:
-        q, kc, vc, nk, nv = kv_case(b, h, t, dh, seed=t + bits)
+    for shape, bits in plan:
+        b, h, t, dh = shape[:4]
+        hkv = shape[4] if len(shape) > 4 else h
+        (q, kc, vc, nk, nv), judged = case_arrays(b, h, t, dh, bits, hkv)
         k_parts, v_parts = quantize_cache_oracle(kc, bits), quantize_cache_oracle(vc, bits)
-        label = f"B={b} H={h} T={t} DH={dh} {bits}-bit"
+        label = f"B={b} H={h} T={t} DH={dh} {bits}-bit" + (f" HKV={hkv}" if hkv != h else "")
         evidence.checks.append(CaseEvidence(
             label=f"{label} GPU quantizer cache bytes identical to the canonical quantizer",
             passed=gpu_cache_identical(kc, bits, k_parts)))
-        ref, tol = reference_and_tolerance("kv_attention", kv_inputs(q, kc, vc, nk, nv, bits))
+        ref, tol = reference_and_tolerance("kv_attention", judged)
         subs = {"T": "half", "BITS": bits, "DH": dh}
         if (bits, dh) not in grouped:
             grouped[(bits, dh)] = (specialize(template, subs), [], [])
@@ -81,7 +100,7 @@ def verify(runner: HipRunner, *, cases=None, out=print) -> GateEvidence:
                                "k_biases": k_parts[2], "v_wq": v_parts[0],
                                "v_scales": v_parts[1], "v_biases": v_parts[2],
                                "new_k": nk, "new_v": nv},
-                       params={"b_rows": b, "n_heads": h, "t_cached": t, "n_kv_heads": h,
+                       params={"b_rows": b, "n_heads": h, "t_cached": t, "n_kv_heads": hkv,
                                "t_stride": t},
                        output_shapes=[((b, h, dh), "float16")], label=label)
         group_cases.append(case)
