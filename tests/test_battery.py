@@ -47,3 +47,42 @@ def test_kv_mutants_compile_for_gfx950(name):
             pytest.skip(str(error))
         raise
     assert len(code) > 0
+
+
+def test_each_moe_mutant_is_the_control_plus_one_fault():
+    from tests.gates import battery_moe as M
+
+    sources = {name: M.mutant_spec(name, 16).source for name in M.MUTANTS}
+    assert len(set(sources.values())) == len(M.MUTANTS)
+    for src in sources.values():
+        assert src.endswith(M.TEMPLATE)
+    with pytest.raises(AssertionError):
+        M.mutant_spec("control", M.MAX_E + 1)
+
+
+@pytest.mark.parametrize("name", ["control", "top-1", "ties-high", "softmax-after-topk"])
+def test_moe_mutants_compile_for_gfx950(name):
+    from tests.gates import battery_moe as M
+
+    try:
+        code = rtc.compile_source(M.mutant_spec(name, 8).source)
+    except rtc.CompileError as error:
+        if "not loadable" in str(error):
+            pytest.skip(str(error))
+        raise
+    assert len(code) > 0
+
+
+def test_moe_battery_plan_is_the_gates():
+    """Same shapes and modes as the gate; constant_rows rows are all near-ties
+    (so only the dispatch rule can see a tie-break fault there)."""
+    from tests.gates import battery_moe as M
+    from tests.gates.pack_moe_dispatch import VERIFY_SHAPES
+
+    plan = M.cases()
+    metas = [m for ms in plan.values() for m in ms]
+    assert len(metas) == 2 * len(VERIFY_SHAPES)
+    for m in metas:
+        if m["label"].startswith("constant_rows"):
+            assert not m["clean"].any()
+        assert m["want"].shape == (m["n"], M.TOP_K)

@@ -94,3 +94,19 @@ def test_kv_mutation_battery():
                  "gqa-modulo"):
         assert table[name]["caught"], (name, table[name])
     assert not table["no-max-shift"]["caught"], table["no-max-shift"]
+
+
+def test_moe_mutation_battery():
+    """The MoE gate's cases against run-time compiled routers: the control
+    passes; the unnormalised gates, the off-by-one expert, top-1 and the
+    high-index tie-break are caught; softmax over the chosen logits is the
+    equivalent mutant and escapes."""
+    from tests.gates import battery_moe
+
+    table = battery_moe.run_battery(HipRunner(repeats=1))
+    print({n: (r["caught"], r["by"], round(r["worst_err_over_tol"], 3)) for n, r in table.items()})
+    assert not table["control"]["caught"], table["control"]
+    for name in ("not-renormalised", "expert-offset", "top-1", "ties-high"):
+        assert table[name]["caught"], (name, table[name])
+    assert "dispatch" in table["ties-high"]["by"]
+    assert not table["softmax-after-topk"]["caught"], table["softmax-after-topk"]
