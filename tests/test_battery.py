@@ -1,4 +1,4 @@
-"""The qmv mutation battery's host side: every mutant differs from the
+"""The mutation batteries' host side: every mutant differs from the
 control by its own fault and compiles for gfx950 (hiprtc, no device). The
 scoring on the GPU is tests/test_gates_gpu.py."""
 
