@@ -12,6 +12,9 @@
 //   permute      one block: stable counting sort of the n*k (token, slot)
 //                pairs by expert, plus the list of routed ("active")
 //                experts and each pair's position (inverse permutation).
+//                For a few pairs on the matrix-core path this launch is
+//                folded into the gate/up launch: each block builds its own
+//                expert's part of the same tables in LDS (block_route).
 //   expert gemv  one block per (active expert, rows): the expert's weight
 //                rows stream from HBM once for all of that expert's tokens
 //                (the reference reads each expert once per token, :101-129).
@@ -262,7 +265,103 @@ struct ExpertArgs {
   const int32_t* active;   // [1 + E]
   float* y;                // [pairs][d_out] fp32, pair order
   int k, d_in, d_out;
+  // In-block routing (gate/up launch, pairs <= kFusedPairs): the flat expert
+  // indices in, and the permute kernel's tables out for the launches after.
+  const uint32_t* idx;     // [pairs]
+  int pairs, n_experts;
+  int32_t* t_offsets;      // [E+1]: entries e and e + 1 of every routed e
+  int32_t* t_perm;         // [pairs]
+  int32_t* t_active;       // [1 + E]
+  int32_t* t_slot_of;      // [pairs]
 };
+
+// Pairs (n * k) up to which the gate/up launch builds its routing in-block.
+constexpr int kFusedPairs = 512;
+
+struct BlockRoute {
+  int e, p0, p1;           // the expert and its segment [p0, p1) of the sorted order
+  const int32_t* seg;      // LDS: the segment's flat pair indices, in flat order
+};
+
+// The permute kernel's result for one expert, built by one block from the
+// flat indices: e is the act-th routed expert in ascending order, its pairs
+// are the flat indices i with idx[i] == e in flat order (a stable sort),
+// and p0 counts the valid pairs routed to experts below e. Every block of
+// the launch builds the same table from the same indices; the first row
+// block of each expert also writes its entries of offsets, active, perm and
+// slot_of, the tables the down projection and the scatter read; block
+// (0, 0) writes the count of routed experts and the -1 slots of invalid
+// indices. False for a block past the routed experts. Called by every
+// thread of the block.
+__device__ bool block_route(const ExpertArgs& a, int act, BlockRoute& br) {
+  __shared__ uint32_t tile[kFusedPairs];
+  __shared__ uint32_t routed[kMaxExperts / 32];
+  __shared__ int32_t seg[kFusedPairs];
+  __shared__ int s_e, s_total, s_p0, s_n;
+  const int pairs = a.pairs, n_experts = a.n_experts;
+  for (int w = threadIdx.x; w < kMaxExperts / 32; w += kBlock) routed[w] = 0u;
+  __syncthreads();
+  for (int i = threadIdx.x; i < pairs; i += kBlock) {
+    const uint32_t e = a.idx[i];
+    tile[i] = e;
+    if (e < (uint32_t)n_experts) atomicOr(&routed[e >> 5], 1u << (e & 31));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int seen = 0, found = -1;
+    for (int w = 0; w < (n_experts + 31) / 32; ++w) {
+      uint32_t m = routed[w];
+      const int c = __popc(m);
+      if (found < 0 && act < seen + c) {
+        for (int skip = act - seen; skip > 0; --skip) m &= m - 1u;  // drop the lowest set bit
+        found = 32 * w + __ffs(m) - 1;
+      }
+      seen += c;
+    }
+    s_e = found;
+    s_total = seen;
+  }
+  __syncthreads();
+  const int e = s_e;
+  if (blockIdx.x == 0 && act == 0) {  // also when no pair names a valid expert
+    if (threadIdx.x == 0) a.t_active[0] = s_total;
+    for (int i = threadIdx.x; i < pairs; i += kBlock)
+      if (tile[i] >= (uint32_t)n_experts) a.t_slot_of[i] = -1;
+  }
+  if (e < 0) return false;  // block-uniform
+  if (threadIdx.x < kWave) {  // wave 0: ballot compaction, 64 pairs a round
+    const int lane = threadIdx.x;
+    const unsigned long long below_lane = (1ull << lane) - 1ull;
+    int lower = 0, mine = 0;
+    for (int i0 = 0; i0 < pairs; i0 += kWave) {  // wave-uniform
+      const int i = i0 + lane;
+      const uint32_t ti = i < pairs ? tile[i] : 0xffffffffu;
+      const unsigned long long hit = __ballot(ti == (uint32_t)e);
+      const unsigned long long low = __ballot(ti < (uint32_t)e);
+      if (ti == (uint32_t)e) seg[mine + __popcll(hit & below_lane)] = i;
+      mine += __popcll(hit);
+      lower += __popcll(low);
+    }
+    if (lane == 0) {
+      s_p0 = lower;
+      s_n = mine;
+    }
+  }
+  __syncthreads();
+  br = BlockRoute{e, s_p0, s_p0 + s_n, seg};
+  if (blockIdx.x == 0) {
+    for (int r = threadIdx.x; r < s_n; r += kBlock) {
+      a.t_perm[br.p0 + r] = seg[r];
+      a.t_slot_of[seg[r]] = br.p0 + r;
+    }
+    if (threadIdx.x == 0) {
+      a.t_offsets[e] = br.p0;
+      a.t_offsets[e + 1] = br.p1;  // the next routed expert writes the same value
+      a.t_active[1 + act] = e;
+    }
+  }
+  return true;
+}
 
 constexpr int kMT = 4;  // tokens per pass of an expert's rows
 constexpr int kRW = 2;  // rows per wave
@@ -515,7 +614,7 @@ struct ExpertStep {
 // KQ waves share one tile's steps (KQ = 4: one tile per block, for long
 // rows) or each wave runs all of its own tile's steps (KQ = 1: four tiles per
 // block share one staging of the activations, for short rows).
-template <int BITS, bool SWIGLU, bool F32IN, int KQ>
+template <int BITS, bool SWIGLU, bool F32IN, int KQ, bool ROUTE = false>
 __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
   using S = MfmaShape<BITS, kEMT>;
   constexpr int NP = SWIGLU ? 2 : 1;            // projections per tile
@@ -524,10 +623,23 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
   constexpr int RS = KQ == 1 ? 4 : 2;           // steps in flight per wave
   extern __shared__ __align__(16) uint4 lds[];
   __shared__ float red[kWaves][NP][kEMT][16];
+  static_assert(!ROUTE || (SWIGLU && !F32IN), "in-block routing is the gate/up launch's");
   const int act = blockIdx.y;
-  if (act >= a.active[0]) return;  // block-uniform
-  const int e = a.active[1 + act];
-  const int p0 = a.offsets[e], p1 = a.offsets[e + 1];
+  int e, p0, p1;
+  const int32_t* seg = nullptr;  // ROUTE: the expert's flat pair indices (LDS)
+  if constexpr (ROUTE) {
+    BlockRoute br;
+    if (!block_route(a, act, br)) return;  // block-uniform
+    e = br.e;
+    p0 = br.p0;
+    p1 = br.p1;
+    seg = br.seg;
+  } else {
+    if (act >= a.active[0]) return;  // block-uniform
+    e = a.active[1 + act];
+    p0 = a.offsets[e];
+    p1 = a.offsets[e + 1];
+  }
   const int G = a.d_in / 64;                 // a multiple of 4 (checked by the launcher)
   const int steps = G / S::kNB;
   const int m_stride = G * kEGroupSlots + 1;  // slots per A row
@@ -594,7 +706,8 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
         float sum = 0.0f;
         u32x4 v[8];
         const bool live = m < nt;
-        const int tok = live ? a.perm[q0 + m] / a.k : 0;
+        const int pair = live ? (ROUTE ? seg[q0 - p0 + m] : a.perm[q0 + m]) : 0;
+        const int tok = pair / a.k;
         const uint32_t* src = reinterpret_cast<const uint32_t*>(a.x + (size_t)tok * a.d_in + g * 64);
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -841,14 +954,22 @@ int check_route_args(int n, int n_experts, int k) {
   return KVP_OK;
 }
 
+// Matrix cores take the experts at 4 and 8 bits: four groups per step, at
+// most 16 steps (d_in <= 4096). KVP_MOE_VALU forces the VALU kernels.
+bool mfma_experts(int bits, int d_in) {
+  const int G = d_in / 64;
+  return (bits == 4 || bits == 8) && G % 4 == 0 && G <= 64 && getenv("KVP_MOE_VALU") == nullptr;
+}
+
+// a.idx set: the gate/up launch routes in-block (matrix-core path only).
 template <int BITS>
 int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f32_input,
                    hipStream_t st) {
   using Gm = Geom<BITS>;
   const int G = a.d_in / 64;
+  const bool route = a.idx != nullptr;
   if constexpr (BITS == 4 || BITS == 8) {
-    // Matrix cores: four groups per step, at most 16 steps (d_in <= 4096).
-    if (G % 4 == 0 && G <= 64 && getenv("KVP_MOE_VALU") == nullptr) {
+    if (mfma_experts(BITS, a.d_in)) {
       const size_t lds = ((size_t)kEMT * (G * kEGroupSlots + 1) + 8) * 16 + (size_t)G * kEMT * 8;
       const int tiles = (a.d_out + 15) / 16;
       // One wave per tile and four tiles per block for short rows (at most
@@ -860,19 +981,24 @@ int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f3
       const char* kq_env = getenv("KVP_MOE_KQ");
       const bool short_rows = kq_env ? atoi(kq_env) == 1 : (G / 4 <= 4 || max_active >= 32);
       const dim3 grid(short_rows ? (tiles + 3) / 4 : tiles, max_active);
-#define KVP_EXPERT(SW, F32, KQ)                                                               \
-  hipLaunchKernelGGL((expert_mfma_kernel<BITS, SW, F32, KQ>), grid, dim3(kBlock), lds, st, a)
+#define KVP_EXPERT(SW, F32, KQ, RT)                                                           \
+  hipLaunchKernelGGL((expert_mfma_kernel<BITS, SW, F32, KQ, RT>), grid, dim3(kBlock), lds, st, a)
+      if (route && !(swiglu_f16 && !f32_input))
+        return set_error(KVP_INVALID, "kvp_moe: in-block routing is for the gate/up launch");
       if (f32_input) {
-        if (short_rows) KVP_EXPERT(false, true, 1); else KVP_EXPERT(false, true, 4);
+        if (short_rows) KVP_EXPERT(false, true, 1, false); else KVP_EXPERT(false, true, 4, false);
+      } else if (swiglu_f16 && route) {
+        if (short_rows) KVP_EXPERT(true, false, 1, true); else KVP_EXPERT(true, false, 4, true);
       } else if (swiglu_f16) {
-        if (short_rows) KVP_EXPERT(true, false, 1); else KVP_EXPERT(true, false, 4);
+        if (short_rows) KVP_EXPERT(true, false, 1, false); else KVP_EXPERT(true, false, 4, false);
       } else {
-        if (short_rows) KVP_EXPERT(false, false, 1); else KVP_EXPERT(false, false, 4);
+        if (short_rows) KVP_EXPERT(false, false, 1, false); else KVP_EXPERT(false, false, 4, false);
       }
 #undef KVP_EXPERT
       return check_launch("kvp_moe expert gemv (matrix cores)");
     }
   }
+  if (route) return set_error(KVP_INVALID, "kvp_moe: in-block routing needs the matrix cores");
   const dim3 grid((a.d_out + kRowsPerBlock - 1) / kRowsPerBlock, max_active);
   if (f32_input) {
     hipLaunchKernelGGL(expert_f32_kernel<BITS>, grid, dim3(kBlock), 0, st, a);
@@ -1034,9 +1160,15 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
   float* h = reinterpret_cast<float*>(ws + L.h);
   float* y = reinterpret_cast<float*>(ws + L.y);
   const int pairs = n * k;
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, st, idx, offsets, perm, active,
-                     slot_of, pairs, n_experts);
-  if (int rc = check_launch("kvp_moe_swiglu (permute)")) return rc;
+  // A few pairs on the matrix-core path: the gate/up launch builds the
+  // permutation in-block (KVP_MOE_PERMUTE forces the permute launch).
+  const bool route_in_block = pairs <= kFusedPairs && mfma_experts(bits, d_model) &&
+                              getenv("KVP_MOE_PERMUTE") == nullptr;
+  if (!route_in_block) {
+    hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, st, idx, offsets, perm, active,
+                       slot_of, pairs, n_experts);
+    if (int rc = check_launch("kvp_moe_swiglu (permute)")) return rc;
+  }
   const int max_active = pairs < n_experts ? pairs : n_experts;
 
   ExpertArgs a{};
@@ -1054,6 +1186,15 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
   a.k = k;
   a.d_in = d_model;
   a.d_out = d_ffn;
+  if (route_in_block) {
+    a.idx = idx;
+    a.pairs = pairs;
+    a.n_experts = n_experts;
+    a.t_offsets = offsets;
+    a.t_perm = perm;
+    a.t_active = active;
+    a.t_slot_of = slot_of;
+  }
   if (int rc = launch_experts_bits(bits, a, max_active, true, false, st)) return rc;
 
   ExpertArgs dn{};

@@ -247,3 +247,34 @@ def test_one_token_at_every_width(bits):
     out = run_swiglu(x, mats, idx, gate, bits, "float32")
     v = judge_swiglu(x, mats, idx, gate, out, None, "float32")
     assert v.ok, (bits, v)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_in_block_routing_equals_the_permute_launch(bits, monkeypatch):
+    """A few pairs on the matrix cores: the gate/up launch builds the
+    permutation in-block. Its output is bit-identical to the separate
+    permute launch (KVP_MOE_PERMUTE=1), also when one pair names no expert
+    (that pair adds nothing: the reference with its gate zeroed) and when
+    none does (zeros)."""
+    x, mats, logits = swiglu_case(6, 16, 512, 256, bits, seed=70 + bits)
+    idx, gate = route_topk(logits, 4)
+    idx = idx.astype(np.uint32)
+    bad = idx.copy()
+    bad[2, 1] = 16
+    none = np.full_like(idx, 99)
+    outs = {}
+    for name, ids in (("routed", idx), ("one-invalid", bad), ("none-valid", none)):
+        monkeypatch.delenv("KVP_MOE_PERMUTE", raising=False)
+        fused = run_swiglu(x, mats, ids, gate, bits, "float32")
+        monkeypatch.setenv("KVP_MOE_PERMUTE", "1")
+        separate = run_swiglu(x, mats, ids, gate, bits, "float32")
+        assert np.array_equal(fused, separate), name
+        outs[name] = fused
+    monkeypatch.delenv("KVP_MOE_PERMUTE", raising=False)
+    assert not np.any(outs["none-valid"])
+    v = judge_swiglu(x, mats, idx, gate, outs["routed"], None, "float32")
+    assert v.ok, v
+    fixed, g0 = idx.copy(), gate.copy()
+    fixed[2, 1], g0[2, 1] = 0, 0.0
+    v = judge_swiglu(x, mats, fixed, g0, outs["one-invalid"], None, "float32")
+    assert v.ok, v
