@@ -20,14 +20,16 @@ reference's own contracts in the way the reference's tests already do:
 - ``permute_by_expert``: the stable counting sort of (token, slot) pairs by
   expert the dispatch kernels consume (closed form).
 - ``swiglu_*``: the gate/up/down expert MLP of config 5. The reference has one
-  linear per expert, so this composition is PARITY UNPINNED against the
-  reference; it is pinned only against a torch fp64 evaluation of the same
-  formula (``silu(x Wg^T) * (x Wu^T)`` then ``Wd``) and, per projection, by the
+  linear per expert and no such composition; each projection follows the
   quantized_matmul contract.
 
 Parity: kv wrappers inherit ``kv_reference``'s pins; ``route_topk`` is pinned by
 brute force (sorting by (-p, index)) and torch ``sort(stable=True)``;
-``permute_by_expert`` by brute force.
+``permute_by_expert`` by brute force; ``swiglu_reference`` by a closed form
+(experts that dequantize to scaled permutation matrices, silu per element)
+and invariants (slot order, gate linearity, a repeated expert, zero gates),
+``swiglu_tolerance`` by admitting its fp32 members and rejecting planted
+mistakes (tests/test_oracle_swiglu.py).
 """
 
 from __future__ import annotations
