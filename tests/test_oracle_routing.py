@@ -9,7 +9,9 @@ permute_by_expert) against what the definitions fix independently:
   shift invariance, and renormalised gates that sum to one in the top-k's
   probability ratios;
 - the permutation: brute force (sorted on (expert, flat index)) and the
-  counting-sort offsets.
+  counting-sort offsets;
+- moe_reference (routing then combine): a closed form on constant router
+  rows and permutation-matrix experts.
 """
 
 from __future__ import annotations
@@ -87,3 +89,26 @@ def test_permutation_is_the_brute_force_stable_sort(n, k, e):
     assert list(perm) == sorted(range(n * k), key=lambda i: (flat[i], i))
     counts = [int((flat == x).sum()) for x in range(e)]
     assert list(offsets) == [sum(counts[:x]) for x in range(e + 1)]
+
+
+def test_moe_reference_closed_form_on_permutation_experts():
+    """Constant router rows make every logit equal: routing is experts 0 and
+    1 (ties low) at gates 1/2 each. Experts a_e P_e (P_e a cyclic shift by
+    s_e) then give out[i] = (a_0 x[i + s_0] + a_1 x[i + s_1]) / 2."""
+    from oracle.native_ops import moe_reference
+
+    d, e = 64, 4
+    shifts, amps = (3, 10, 17, 29), (0.5, 1.25, 2.0, 0.75)
+    experts = np.zeros((e, d, d))
+    for j in range(e):
+        experts[j, np.arange(d), (np.arange(d) + shifts[j]) % d] = amps[j]
+    x = np.random.default_rng(9).standard_normal((3, d)).astype(np.float16)
+    router = np.full((e, d), 0.03125, dtype=np.float16)
+    out = moe_reference({"x": x, "router": router, "experts": experts})
+    x64 = x.astype(np.float64)
+    want = 0.5 * (amps[0] * np.roll(x64, -shifts[0], axis=1)
+                  + amps[1] * np.roll(x64, -shifts[1], axis=1))
+    assert np.max(np.abs(out - want)) <= 1e-12 * np.max(np.abs(want))
+    transposed = experts.transpose(0, 2, 1).copy()
+    wrong = moe_reference({"x": x, "router": router, "experts": transposed})
+    assert np.max(np.abs(wrong - want)) > 1e-2 * np.max(np.abs(want))
