@@ -114,7 +114,8 @@ class RoutedLinear(nn.Module):
         m = x.numel() // d_in
         if not wide_qmv.should_dispatch(m, inner.bits, inner.d_out, d_in):
             return f"m-{m}-outside-dispatch-{inner.d_out}x{d_in}"
-        if not x.is_cuda or x.device != inner.weight.device:
+        if not x.is_cuda or any(p.device != x.device
+                                for p in (inner.weight, inner.scales, inner.biases)):
             return f"device-{x.device}"
         return None
 
@@ -191,12 +192,11 @@ class QuantizedKVCache:
 
     def _quantize_into(self, dst: tuple, x: torch.Tensor, at: int) -> None:
         hkv, n, dh = x.shape[1], x.shape[2], x.shape[3]
-        src = x.reshape(hkv * n, dh).to(torch.float16).contiguous()
-        parts = (torch.empty((hkv * n, dh * self.bits // 32), dtype=torch.int32, device=x.device),
-                 torch.empty((hkv * n, dh // self.group_size), dtype=torch.float16,
-                             device=x.device),
-                 torch.empty((hkv * n, dh // self.group_size), dtype=torch.float16,
-                             device=x.device))
+        dev = dst[0].device
+        src = x.reshape(hkv * n, dh).to(device=dev, dtype=torch.float16).contiguous()
+        parts = (torch.empty((hkv * n, dh * self.bits // 32), dtype=torch.int32, device=dev),
+                 torch.empty((hkv * n, dh // self.group_size), dtype=torch.float16, device=dev),
+                 torch.empty((hkv * n, dh // self.group_size), dtype=torch.float16, device=dev))
         lib.check(lib.load().kvp_quantize_affine(src.data_ptr(), hkv * n, dh, self.bits,
                                                  parts[0].data_ptr(), parts[1].data_ptr(),
                                                  parts[2].data_ptr(), _stream()))
@@ -204,8 +204,18 @@ class QuantizedKVCache:
             d[0, :, at:at + n] = p.reshape(hkv, n, -1)
 
     def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:
-        """Quantize (1, HKV, L, DH) new entries into positions offset .. offset + L."""
+        """Quantize (1, HKV, L, DH) new entries into positions offset .. offset + L
+        with the library's GPU quantizer (the cache must be on a cuda device;
+        the entries move there)."""
+        if not self.keys[0].is_cuda:
+            raise ValueError(f"append quantizes on the GPU: this cache is on {self.keys[0].device}")
+        want = (1, self.n_kv_heads, keys.shape[2], self.head_dim)
+        if tuple(keys.shape) != want or tuple(values.shape) != want:
+            raise ValueError(f"append takes keys and values of shape {want}, got "
+                             f"{tuple(keys.shape)} and {tuple(values.shape)}")
         n = keys.shape[2]
+        if n == 0:
+            return
         if self.offset + n > self.max_len:
             raise ValueError(f"cache of {self.max_len} positions cannot take {n} more at "
                              f"{self.offset}")
@@ -260,6 +270,8 @@ class KvDoor:
             return "nonstandard-scale"
         if not queries.is_cuda:
             return f"device-{queries.device}"
+        if any(p.device != queries.device for p in (*cache.keys, *cache.values)):
+            return f"cache-device-{cache.keys[0].device}"
         return None
 
     @staticmethod
@@ -267,8 +279,8 @@ class KvDoor:
         b, h, _, d = queries.shape
         hkv = cache.n_kv_heads
         q = queries.reshape(b, h, d).contiguous()
-        nk = new_k.reshape(b, hkv, d).to(torch.float16).contiguous()
-        nv = new_v.reshape(b, hkv, d).to(torch.float16).contiguous()
+        nk, nv = (t.reshape(b, hkv, d).to(device=queries.device, dtype=torch.float16).contiguous()
+                  for t in (new_k, new_v))
         t_cached = torch.full((b,), cache.offset, dtype=torch.int32, device=queries.device)
         out = torch.empty((b, h, d), dtype=torch.float16, device=queries.device)
         L = lib.load()
@@ -297,7 +309,8 @@ class KvDoor:
         t = k.shape[2]
         if length > 1:  # causal over the new entries
             pos = torch.arange(t, device=queries.device)
-            allowed = pos[None, :] <= (t - length + torch.arange(length, device=queries.device))[:, None]
+            rows = t - length + torch.arange(length, device=queries.device)
+            allowed = pos[None, :] <= rows[:, None]
             scores = scores.masked_fill(~allowed, float("-inf"))
         p = torch.softmax(scores, dim=-1)
         return torch.matmul(p, v).to(queries.dtype)

@@ -141,3 +141,13 @@ def test_kv_refusals_and_the_stock_step_against_the_oracle():
     ref = kv_reference_gqa(q, k_raw, v_raw, nk, nv, bits)
     err = np.max(np.abs(out.reshape(1, h, dh).numpy().astype(np.float64) - ref))
     assert err <= 4 * 9.77e-4 * np.max(np.abs(ref))
+
+
+def test_cpu_cache_refuses_append_and_shapes_are_checked():
+    """append quantizes with the GPU library: a CPU cache refuses it before
+    any call, and mis-shaped entries are named."""
+    cache = QuantizedKVCache(2, 64, 4, 16, device="cpu")
+    k = torch.zeros((1, 2, 3, 64))
+    with pytest.raises(ValueError, match="on the GPU"):
+        cache.append(k, k)
+    assert cache.offset == 0

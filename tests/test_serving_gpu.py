@@ -72,17 +72,21 @@ def test_kv_door_reads_the_logical_length_not_the_stride(bits, dh, gqa):
         part[0, :, t:] = 7 if part.dtype == torch.int32 else 1000.0
     cache.append(torch.from_numpy(k_raw[None, :, :60]).cuda(),
                  torch.from_numpy(v_raw[None, :, :60]).cuda())
-    cache.append(torch.from_numpy(k_raw[None, :, 60:]).cuda(),
-                 torch.from_numpy(v_raw[None, :, 60:]).cuda())
+    # entries given on the host move to the cache's device; an empty append is a no-op
+    cache.append(torch.from_numpy(k_raw[None, :, 60:]), torch.from_numpy(v_raw[None, :, 60:]))
+    cache.append(torch.zeros((1, hkv, 0, dh)), torch.zeros((1, hkv, 0, dh)))
     assert cache.offset == t
     art = canonical_quantize(k_raw.reshape(-1, dh), QuantContract(bits=bits, group_size=64))
     assert np.array_equal(cache.keys[0][0, :, :t].cpu().numpy().view(np.uint32).reshape(-1, dh * bits // 32),
                           pack_codes(art.q, bits))
     door = KvDoor()
     scale = 1 / math.sqrt(dh)
-    out = door(torch.from_numpy(q).cuda().reshape(1, h, 1, dh), cache,
-               torch.from_numpy(nk).cuda().reshape(1, hkv, 1, dh),
-               torch.from_numpy(nv).cuda().reshape(1, hkv, 1, dh), scale)
+    qd = torch.from_numpy(q).cuda().reshape(1, h, 1, dh)
+    host_cache = QuantizedKVCache(hkv, dh, bits, stride, device="cpu")
+    assert door.ineligible(qd, host_cache, scale) == "cache-device-cpu"
+    # the step's own entry may come from the host: it moves to the queries' device
+    out = door(qd, cache, torch.from_numpy(nk).reshape(1, hkv, 1, dh),
+               torch.from_numpy(nv).reshape(1, hkv, 1, dh), scale)
     torch.cuda.synchronize()
     assert door.calls == 1 and not door.fallbacks
     ref = kv_reference_gqa(q, k_raw, v_raw, nk, nv, bits)
