@@ -168,8 +168,11 @@ int kvp_moe_dispatch(const void* x, const uint32_t* idx, const float* gate,
  * gate_/up_ weights [n_experts][d_ffn][d_model], down [n_experts][d_model][d_ffn],
  * each with fp16 scales/biases per 64-code group; x fp16 [n][d_model];
  * out [n][d_model]. Experts are visited once per step: the (token, slot)
- * pairs are grouped by expert (kvp_moe_permute) so each expert's weights
- * stream from HBM once however many tokens chose it.
+ * pairs are grouped by expert (kvp_moe_permute's stable order; for
+ * n * k <= 512 on the 4/8-bit matrix-core path the gate/up launch builds
+ * that order itself) so each expert's weights stream from HBM once however
+ * many tokens chose it. A pair naming no expert (idx >= n_experts) adds
+ * nothing.
  * n * k <= 8192. workspace: kvp_moe_swiglu_workspace_bytes(n, k, n_experts,
  * d_model, d_ffn). */
 size_t kvp_moe_swiglu_workspace_bytes(int n, int k, int n_experts, int d_model, int d_ffn);
