@@ -278,3 +278,21 @@ def test_in_block_routing_equals_the_permute_launch(bits, monkeypatch):
     fixed[2, 1], g0[2, 1] = 0, 0.0
     v = judge_swiglu(x, mats, fixed, g0, outs["one-invalid"], None, "float32")
     assert v.ok, v
+
+
+@pytest.mark.parametrize("n", [64, 65])
+def test_in_block_routing_limit(n, monkeypatch):
+    """n * k = 512 pairs is the largest in-block routing (bit-identical to
+    the permute launch); 520 takes the permute launch. Both against the
+    oracle on three tokens."""
+    x, mats, logits = swiglu_case(n, 128, 512, 256, 4, seed=80 + n)
+    idx, gate = route_topk(logits, 8)
+    idx = idx.astype(np.uint32)
+    monkeypatch.delenv("KVP_MOE_PERMUTE", raising=False)
+    out = run_swiglu(x, mats, idx, gate, 4, "float32")
+    if n * 8 <= 512:
+        monkeypatch.setenv("KVP_MOE_PERMUTE", "1")
+        assert np.array_equal(out, run_swiglu(x, mats, idx, gate, 4, "float32"))
+        monkeypatch.delenv("KVP_MOE_PERMUTE")
+    v = judge_swiglu(x, mats, idx, gate, out, [0, n // 2, n - 1], "float32")
+    assert v.ok, v
