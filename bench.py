@@ -23,6 +23,14 @@ The other BASELINE configurations ride in the same line: the qmv ones
 "secondary", KV decode (configs 3 and 4 and the 32k case) under "kv_decode",
 and the MoE expert layer (config 5) under "moe".
 
+CPU paths (skipped with ``--no-cpu``): ``cpu_baseline`` times the numpy
+control path of the headline (fp32 dequant + BLAS) and adds
+``matmul_only_value``, BLAS alone on weights dequantized beforehand (an upper
+bound for any CPU path), and the BLAS vendor. Every KV and MoE row carries
+``cpu``: a numpy port of the reference CPU path on the same stored
+artefacts, dequantized per call as the GPU path does, checked against the
+verified GPU output and timed over a bounded sample.
+
 ``--gpus N`` with N > 1 exits: this build measures one GPU.
 """
 
@@ -133,6 +141,7 @@ class KvWorkload:
         k = quantize_affine(DeviceArray.from_host(self.k_raw.reshape(shape)), bits)
         v = quantize_affine(DeviceArray.from_host(self.v_raw.reshape(shape)), bits)
         hip.synchronize()
+        self._parts = (k, v)
         self.bytes = kv_attention.algorithmic_bytes(self.lengths, n_heads, n_kv_heads, head_dim,
                                                     bits)
         cache_bytes = sum(a.nbytes for a in (*k, *v))
@@ -163,6 +172,12 @@ class KvWorkload:
         self.step(None)
         hip.synchronize()
         return self.out.to_host()
+
+    def cpu_fn(self):
+        """The CPU decode step on the same stored caches (downloaded once)."""
+        k, v = ([a.to_host() for a in parts] for parts in self._parts)
+        return lambda: kv_cpu_path(self.q, self.nk, self.nv, k, v, self.lengths, self.bits,
+                                   self.per_sequence)
 
     def check(self, got):
         """max |gpu - fp64 reference| against 4 eps16 max|ref|, per sequence."""
@@ -199,6 +214,7 @@ class MoeWorkload:
                                   (n_experts, d_model, d_ffn))]
         mats = [quantize_affine(DeviceArray.from_host(w), bits) for w in self.raw]
         hip.synchronize()
+        self._mats = mats
         set_bytes = sum(a.nbytes for m in mats for a in m)
         copies = max(2, -(-ROTATION_BYTES // set_bytes))
         self.dx = DeviceArray.from_host(self.x)
@@ -234,6 +250,11 @@ class MoeWorkload:
         self.step(None)
         hip.synchronize()
         return self.out.to_host()
+
+    def cpu_fn(self):
+        """The CPU MoE step from the same logits and stored experts."""
+        host = [tuple(a.to_host() for a in m) for m in self._mats]
+        return lambda: moe_cpu_path(self.x, self.logits, self.k, *host, self.bits)
 
     def check(self, got, tokens=(0,)):
         """Error over 4 eps16 max|ref| on a few tokens (fp64 SwiGLU reference)."""
@@ -301,6 +322,93 @@ def cpu_baseline(fn, budget_s: float = 12.0, min_reps: int = 3):
         fn()
         times.append(time.perf_counter() - t0)
     return min(times), float(np.median(times)), len(times)
+
+
+def host_dequant(words: np.ndarray, scales: np.ndarray, biases: np.ndarray, bits: int):
+    """fp32 s * q + b of an MLX-affine artefact held on the host (4- or 8-bit
+    code streams: byte j holds codes 2j, 2j+1 at 4 bits, code j at 8)."""
+    b = np.ascontiguousarray(words).view(np.uint8)
+    if bits == 4:
+        q = np.empty(b.shape[:-1] + (2 * b.shape[-1],), dtype=np.float32)
+        q[..., 0::2] = b & 15
+        q[..., 1::2] = b >> 4
+    elif bits == 8:
+        q = b.astype(np.float32)
+    else:
+        raise ValueError(f"host_dequant: bits={bits}")
+    s = np.repeat(scales.astype(np.float32), 64, axis=-1)
+    return q * s + np.repeat(biases.astype(np.float32), 64, axis=-1)
+
+
+def kv_cpu_path(q, new_k, new_v, k_parts, v_parts, lengths, bits, per_sequence):
+    """The CPU decode step (reference/native_kernels.py:168-221 semantics, fp32
+    numpy + BLAS) from the stored quantized caches: per sequence, dequantize
+    its T rows, scores over T + 1 with the new entry, softmax, values.
+    q (B, H, DH); caches (C, HKV, T_stride, ...) or (HKV, T_stride, ...)."""
+    b, h, dh = q.shape
+    hkv = new_k.shape[1]
+    g = h // hkv
+    scale = np.float32(1.0 / np.sqrt(dh))
+    out = np.empty((b, h, dh), dtype=np.float32)
+    for i, t in enumerate(lengths):
+        sel = (lambda a: a[i][:, :t]) if per_sequence else (lambda a: a[:, :t])
+        kd = host_dequant(*(sel(a) for a in k_parts), bits)          # (HKV, T, DH)
+        vd = host_dequant(*(sel(a) for a in v_parts), bits)
+        qg = q[i].astype(np.float32).reshape(hkv, g, dh)
+        s = np.matmul(qg, kd.transpose(0, 2, 1)) * scale             # (HKV, G, T)
+        s_new = np.einsum("kgd,kd->kg", qg, new_k[i].astype(np.float32)) * scale
+        m = np.maximum(s.max(axis=-1), s_new)
+        p = np.exp(s - m[..., None])
+        p_new = np.exp(s_new - m)
+        o = np.matmul(p, vd) + p_new[..., None] * new_v[i].astype(np.float32)[:, None, :]
+        out[i] = (o / (p.sum(axis=-1) + p_new)[..., None]).reshape(h, dh)
+    return out
+
+
+def moe_cpu_path(x, logits, k, gate_parts, up_parts, down_parts, bits):
+    """The CPU MoE step (reference/native_kernels.py:104-147 semantics at top-k,
+    SwiGLU experts; fp32 numpy + BLAS): softmax over all experts, top-k by
+    probability (ties low), renormalised; each routed expert's three
+    projections dequantized once per step and applied to its tokens."""
+    p = np.exp(logits - logits.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    top = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+    w = np.take_along_axis(p, top, axis=-1)
+    w /= w.sum(axis=-1, keepdims=True)
+    xf = x.astype(np.float32)
+    out = np.zeros((x.shape[0], down_parts[0].shape[1]), dtype=np.float32)
+    for e in np.unique(top):
+        rows, slots = np.nonzero(top == e)
+        wg = host_dequant(*(a[e] for a in gate_parts), bits)
+        wu = host_dequant(*(a[e] for a in up_parts), bits)
+        wd = host_dequant(*(a[e] for a in down_parts), bits)
+        gx, ux = xf[rows] @ wg.T, xf[rows] @ wu.T
+        hidden = gx / (1.0 + np.exp(-gx)) * ux
+        np.add.at(out, rows, w[rows, slots][:, None] * (hidden @ wd.T))
+    return out
+
+
+def blas_vendor() -> str:
+    try:
+        return str(np.show_config(mode="dicts")["Build Dependencies"]["blas"]["name"])
+    except Exception:
+        return "unknown"
+
+
+def cpu_row(workload, gpu_out, what: str) -> dict | None:
+    """The CPU path of a KV or MoE row on the same inputs, a bounded sample
+    (about 4 s, at least 2 calls), after a check of its output against the
+    verified GPU output; None (logged) if they disagree."""
+    fn = workload.cpu_fn()
+    ref = np.asarray(gpu_out, dtype=np.float64)
+    got = np.asarray(fn(), dtype=np.float64).reshape(ref.shape)
+    if not np.max(np.abs(got - ref)) <= 4 * 9.77e-4 * np.max(np.abs(ref)):
+        log(f"[bench] CPU path of {workload.name} disagrees with the GPU output; not timed")
+        return None
+    best, med, n = cpu_baseline(fn, budget_s=4.0, min_reps=2)
+    return {"us_per_call": round(best * 1e6, 1), "median_us": round(med * 1e6, 1),
+            "GBps": round(workload.bytes / best / 1e9, 3), "calls": n, "cores": blas_threads(),
+            "kind": "port", "path": what}
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "qmv_4b_14336x4096_m1.traffic.json"
@@ -394,7 +502,8 @@ def main() -> int:
                dict(lengths=list(np.random.default_rng(0).integers(1024, 32769, 8)), bits=4,
                     per_sequence=True, t_stride=32768)):
         w = KvWorkload(**kw)
-        ratio = w.check(w.gpu_output())
+        got = w.gpu_output()
+        ratio = w.check(got)
         if not ratio <= 1.0:
             log(f"[bench] verify FAILED {w.name}: error {ratio:.2f} x bound")
             continue
@@ -403,13 +512,17 @@ def main() -> int:
         kv.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3), "GBps": round(gbs2, 1),
                    "frac_8TBps": round(gbs2 / PEAK_HBM_GBS, 4), "bytes": w.bytes,
                    "verify_err_over_bound": round(ratio, 4)})
+        if not args.no_cpu:
+            kv[-1]["cpu"] = cpu_row(w, got, "dequantize the stored caches, fp32 scores, "
+                                    "softmax over T + 1, values (native_kernels.py:168-221)")
         log(f"[bench] {kv[-1]}")
         del w
 
     moe_rows = []
     for n in () if args.headline_only else (1, 8, 32):
         w = MoeWorkload(n)
-        ratio = w.check(w.gpu_output(), tokens=(0, n - 1) if n > 1 else (0,))
+        got = w.gpu_output()
+        ratio = w.check(got, tokens=(0, n - 1) if n > 1 else (0,))
         if not ratio <= 1.0:
             log(f"[bench] verify FAILED {w.name}: error {ratio:.2f} x bound")
             continue
@@ -419,6 +532,10 @@ def main() -> int:
                          "GBps": round(gbs3, 1), "frac_8TBps": round(gbs3 / PEAK_HBM_GBS, 4),
                          "unique_experts": w.unique, "bytes": w.bytes,
                          "verify_err_over_bound": round(ratio, 4)})
+        if not args.no_cpu:
+            moe_rows[-1]["cpu"] = cpu_row(w, got, "softmax top-8 routing, each routed expert's "
+                                          "gate/up/down dequantized once, fp32 SwiGLU "
+                                          "(native_kernels.py:104-147 at top-k)")
         log(f"[bench] {moe_rows[-1]}")
         del w
 
@@ -432,6 +549,15 @@ def main() -> int:
                          f"best {best * 1e3:.1f} ms, median {med * 1e3:.1f} ms; "
                          f"host {platform.processor() or platform.machine()}, "
                          f"os.cpu_count()={os.cpu_count()}"}
+        wdq = host_dequant(head.w_q, head.scales, head.biases, 4)
+        x32 = head.x.astype(np.float32)
+        best_mm, _, n_mm = cpu_baseline(lambda: x32 @ wdq.T, budget_s=3.0)
+        del wdq
+        cpu["matmul_only_value"] = round(head.bytes / best_mm / 1e9, 3)
+        cpu["blas"] = blas_vendor()
+        cpu["sample"] += (f"; upper bound: BLAS sgemv alone on the weights dequantized "
+                          f"beforehand, best of {n_mm}, {best_mm * 1e3:.1f} ms "
+                          f"(matmul_only_value)")
         log(f"[bench] cpu baseline: {cpu}")
 
     line = {
