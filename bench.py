@@ -454,7 +454,7 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    from kernelverify_amd import hip, lib
+    from kernelverify_amd import hip, lib, roofline
 
     if hip.device_count() == 0:
         print("bench.py: no HIP device visible", file=sys.stderr)
@@ -486,8 +486,6 @@ def main() -> int:
     # ceiling as well as the spec).
     ceiling = None
     if not args.headline_only:
-        from kernelverify_amd import roofline
-
         c_gbs, c_us = roofline.read_like(head.bytes)
         ceiling = {"GBps": round(c_gbs, 1), "us_per_launch": round(c_us, 3),
                    "frac": round(gbs / c_gbs, 4),
@@ -529,8 +527,6 @@ def main() -> int:
         kv.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3), "GBps": round(gbs2, 1),
                    "frac_8TBps": round(gbs2 / PEAK_HBM_GBS, 4), "bytes": w.bytes,
                    "verify_err_over_bound": round(ratio, 4)})
-        from kernelverify_amd import roofline
-
         kv[-1]["frac_measured_ceiling"] = round(gbs2 / roofline.read_like(w.bytes)[0], 4)
         if not args.no_cpu:
             kv[-1]["cpu"] = cpu_row(w, got, "dequantize the stored caches, fp32 scores, "
