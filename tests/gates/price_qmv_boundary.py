@@ -31,7 +31,7 @@ MAX_CANARY_SPREAD, WIN / LOSS only when the whole ratio interval
 [min(incumbent)/max(ours), max(incumbent)/min(ours)] clears 1.0, else
 REFUSED.
 
-    python -m tests.gates.price_qmv_boundary --out gpurun_out/qmv-boundary-pricing-mi355x.json
+    python -m tests.gates.price_qmv_boundary --out /tmp/qmv-boundary-pricing-mi355x.json
 """
 
 from __future__ import annotations
