@@ -19,7 +19,8 @@ re-targeted to HIP):
   the bytes of ``kernelverify_amd.pack.wide_qmv.algorithmic_bytes``;
   ``roofline.frac`` is against the 8 TB/s spec and
   ``roofline.measured_ceiling`` against back-to-back probe reads of the same
-  bytes per launch (each KV row carries ``frac_measured_ceiling`` alike).
+  bytes per launch (each KV and MoE row carries ``frac_measured_ceiling``
+  alike).
 
 The other BASELINE configurations ride in the same line: the qmv ones
 (config 1's 4096 x 4096, config 2's 8-bit, M = 4/8 and 4096 x 14336) under
@@ -548,6 +549,7 @@ def main() -> int:
                          "GBps": round(gbs3, 1), "frac_8TBps": round(gbs3 / PEAK_HBM_GBS, 4),
                          "unique_experts": w.unique, "bytes": w.bytes,
                          "verify_err_over_bound": round(ratio, 4)})
+        moe_rows[-1]["frac_measured_ceiling"] = round(gbs3 / roofline.read_like(w.bytes)[0], 4)
         if not args.no_cpu:
             moe_rows[-1]["cpu"] = cpu_row(w, got, "softmax top-8 routing, each routed expert's "
                                           "gate/up/down dequantized once, fp32 SwiGLU "
