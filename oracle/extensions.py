@@ -29,7 +29,11 @@ brute force (sorting by (-p, index)) and torch ``sort(stable=True)``;
 (experts that dequantize to scaled permutation matrices, silu per element)
 and invariants (slot order, gate linearity, a repeated expert, zero gates),
 ``swiglu_tolerance`` by admitting its fp32 members and rejecting planted
-mistakes (tests/test_oracle_swiglu.py).
+mistakes (tests/test_oracle_swiglu.py); ``moe_linear_reference`` by a
+closed form on permutation experts and equality with ``moe_reference`` on
+the same routing, ``moe_linear_tolerance`` by admitting an fp32 evaluation
+in another order and rejecting five planted mistakes
+(tests/test_oracle_contract.py).
 """
 
 from __future__ import annotations

@@ -17,11 +17,15 @@ reductions run along DH or T inside one (b, h) row), so long-context cases
 stay within a few hundred MB.
 
 Parity: the reference functions are pinned by the golden records
-(``quant_device_adequacy.json``: ``ref_scale``/``base_tol``) for the qmm path,
-by the reference's own known-answer tests for moe routing, and by the KV
-invariants (batch-row independence, new-entry dominance, T=1, padded prefix,
-GQA = tiled cache) for the KV path, plus a torch fp64
-``scaled_dot_product_attention`` cross-check of ``kv_reference``.
+(``quant_device_adequacy.json``: ``ref_scale``/``base_tol``) for the qmm path
+(tests/test_oracle_golden.py); ``moe_reference`` by a torch fp64 restatement
+of the routing contract and a closed form on permutation experts, and
+``moe_tolerance`` by admitting its members and rejecting five planted
+mistakes (tests/test_oracle_contract.py, tests/test_oracle_routing.py); the
+KV path by the KV invariants (batch-row independence, new-entry dominance,
+T=1, padded prefix, GQA = tiled cache) and a torch fp64
+``scaled_dot_product_attention`` cross-check of ``kv_reference``, with
+``kv_tolerance`` rejecting four planted mistakes (tests/test_oracle_kv.py).
 """
 
 from __future__ import annotations
