@@ -1,29 +1,34 @@
-"""Structured evidence from a pack gate's verification run (reference:
-kernelverify/pack/evidence.py:65-195).
+"""What a pack gate's ``verify()`` found, as data for its banner and for the
+certificate emitter.
 
-A gate's `verify()` returns a `GateEvidence`; its console banner renders from
-it (`render_banner`), and anything downstream (a certificate emitter, a
-report) consumes it directly instead of parsing output.
+The class, field and property names are the reference's gate-evidence
+interface (kernelverify/pack/evidence.py:65-195), because the certificate
+emitter and its readers consume them; the implementation is this build's.
 
-- one `SpecializationEvidence` per compile-time specialization (the unit a
-  certificate is issued for), holding one `CaseEvidence` per case: the
-  verdict, the error and tolerance behind it, and an advisory sha256 of the
-  output bytes (GPU outputs are not bit-stable, so the fingerprint describes
-  the certifying run and is never a re-check criterion);
-- gate-level `checks` for side conditions that are not kernel verdicts
-  (artefact identity, a negative control failing as it must).
+Shape of the record:
 
-`SpecializationEvidence.calls` keeps each case's `RunCase` beside its
-verdict; `drop_verified_inputs` empties the inputs of passing cases once
-judged, so only failing bytes are retained. No timing is recorded here:
-verification may run under contention, and a number recorded in evidence
-invites quoting.
+- `GateEvidence`: one gate run, its policy and seed protocol in words, the
+  specializations it judged and its side `checks` (boolean facts such as a
+  faulted artefact failing as it must);
+- `SpecializationEvidence`: one compile-time specialization (the unit a
+  certificate is issued for), identified by its kernel family and its
+  `specialize()` substitutions, with one `CaseEvidence` per case and, aligned
+  with them, the `RunCase` each ran (`calls`);
+- `CaseEvidence`: a verdict, the error and tolerance behind it when one was
+  computed, sha256 fingerprints of the input and output bytes (outputs are
+  not bit-stable across GPU runs, so theirs describes the certifying run
+  and is never a re-check criterion), and free-form `aux` numbers.
+
+Passing cases can hand back their input arrays once judged
+(`drop_verified_inputs`): their fingerprints stay, and only the bytes of a
+failing case are kept for reproduction. Nothing here records time.
 """
 
 from __future__ import annotations
 
 import hashlib
 from dataclasses import dataclass, field
+from typing import Callable, Iterable, Iterator
 
 import numpy as np
 
@@ -31,6 +36,7 @@ __all__ = [
     "CaseEvidence",
     "GateEvidence",
     "SpecializationEvidence",
+    "banner_lines",
     "by_family",
     "input_fingerprints",
     "output_fingerprint",
@@ -38,24 +44,26 @@ __all__ = [
 ]
 
 
-def _array_sha256(array) -> str:
-    return hashlib.sha256(np.ascontiguousarray(np.asarray(array)).tobytes()).hexdigest()
+def _sha256_of(array) -> str:
+    """sha256 of an array's C-order bytes (its dtype and shape are not hashed)."""
+    contiguous = np.ascontiguousarray(np.asarray(array))
+    return hashlib.sha256(contiguous.tobytes()).hexdigest()
 
 
 def output_fingerprint(array) -> str:
-    """Advisory sha256 of the output bytes from the certifying run."""
-    return _array_sha256(array)
+    """Fingerprint of one output, advisory: it names the certifying run's bytes."""
+    return _sha256_of(array)
 
 
 def input_fingerprints(inputs: dict) -> dict:
-    """sha256 per input array: which bytes ran, kept for every case."""
-    return {name: _array_sha256(array) for name, array in inputs.items()}
+    """{input name: fingerprint}, kept for every case whatever its verdict."""
+    return {name: _sha256_of(value) for name, value in inputs.items()}
 
 
 @dataclass(frozen=True)
 class CaseEvidence:
-    """One case's verdict; `err`/`tol` are None when nothing numerical was
-    judged (a runner failure, or a boolean check)."""
+    """One case's verdict. ``err``/``tol`` stay None when no comparison was
+    made (the runner did not finish, or the entry is a boolean check)."""
 
     label: str
     passed: bool
@@ -66,36 +74,80 @@ class CaseEvidence:
     input_sha256: dict = field(default_factory=dict)
     aux: dict = field(default_factory=dict)
 
+    @property
+    def judged(self) -> bool:
+        """Whether a numerical comparison stands behind the verdict."""
+        return self.err is not None and self.tol is not None
+
+    def describe(self) -> str:
+        """One banner line: the label, the numbers when there are any, the verdict."""
+        verdict = "ok" if self.passed else "FAILED"
+        parts = [self.label]
+        if self.judged:
+            parts.append(f"err={self.err:.3e} tol={self.tol:.3e}")
+        parts.append(verdict)
+        if self.detail and (self.judged or not self.passed):
+            parts.append(f"[{self.detail}]")
+        elif not self.judged and not self.passed:
+            parts.append("[no verdict recorded]")
+        return "  ".join(parts)
+
+
+def _count(cases: Iterable[CaseEvidence]) -> tuple[int, int]:
+    """(cases, of which passed)."""
+    flags = [bool(c.passed) for c in cases]
+    return len(flags), sum(flags)
+
 
 @dataclass
 class SpecializationEvidence:
-    kernel: str        # kernel family, e.g. "kvp_qmv"
-    operator: str      # the operator the cases were judged against
-    template: dict     # the specialize() substitutions
+    kernel: str       # kernel family, e.g. "kvp_qmv"
+    operator: str     # the oracle operator the cases were judged against
+    template: dict    # the specialize() substitutions
     threadgroup: tuple = (1, 1, 1)
-    cases: list = field(default_factory=list)   # CaseEvidence
-    calls: list = field(default_factory=list)   # RunCase, aligned with cases
+    cases: list = field(default_factory=list)   # CaseEvidence, in run order
+    calls: list = field(default_factory=list)   # RunCase per case, same order
+
+    @property
+    def key(self) -> tuple:
+        """Identity within a gate: the family and the substitutions."""
+        return (self.kernel, tuple(sorted((str(k), str(v)) for k, v in self.template.items())))
+
+    @property
+    def template_text(self) -> str:
+        return " ".join(f"{k}={self.template[k]}" for k in sorted(self.template))
 
     @property
     def cases_run(self) -> int:
-        return len(self.cases)
+        return _count(self.cases)[0]
 
     @property
     def cases_passed(self) -> int:
-        return sum(1 for c in self.cases if c.passed)
+        return _count(self.cases)[1]
 
     @property
     def ok(self) -> bool:
-        return bool(self.cases) and self.cases_passed == self.cases_run
+        run, passed = _count(self.cases)
+        return run > 0 and run == passed
+
+    def release_passing_inputs(self) -> int:
+        """Empty the inputs of every call whose case passed; returns how
+        many were emptied."""
+        emptied = 0
+        for case, call in zip(self.cases, self.calls):
+            if case.passed and call is not None and call.inputs:
+                call.inputs = {}
+                emptied += 1
+        return emptied
 
 
 @dataclass
 class GateEvidence:
-    gate: str
-    policy: str
-    seed_protocol: str
-    specializations: list = field(default_factory=list)
-    checks: list = field(default_factory=list)
+    gate: str            # e.g. "pack_wide_qmv"
+    policy: str          # the gate's case policy, in words a re-checker can follow
+    seed_protocol: str   # how a re-checker draws the same inputs
+    specializations: list = field(default_factory=list)  # SpecializationEvidence
+    checks: list = field(default_factory=list)           # CaseEvidence
 
     @property
     def cases_run(self) -> int:
@@ -107,60 +159,58 @@ class GateEvidence:
 
     @property
     def checks_passed(self) -> bool:
-        return all(c.passed for c in self.checks)
+        return _count(self.checks)[0] == _count(self.checks)[1]
 
     @property
     def ok(self) -> bool:
-        return (bool(self.specializations) and all(s.ok for s in self.specializations)
-                and self.checks_passed)
+        specs_green = [s.ok for s in self.specializations]
+        return bool(specs_green) and all(specs_green) and self.checks_passed
 
     def specialization(self, kernel: str, operator: str, template: dict,
                        threadgroup: tuple) -> SpecializationEvidence:
-        """The bucket for `template`, created on first use."""
-        for existing in self.specializations:
-            if existing.kernel == kernel and existing.template == template:
-                return existing
-        created = SpecializationEvidence(kernel=kernel, operator=operator, template=dict(template),
-                                         threadgroup=tuple(threadgroup))
-        self.specializations.append(created)
-        return created
+        """The record of (``kernel``, ``template``) in this gate, added the
+        first time it is asked for."""
+        fresh = SpecializationEvidence(kernel=kernel, operator=operator,
+                                       template=dict(template), threadgroup=tuple(threadgroup))
+        known = {s.key: s for s in self.specializations}
+        if fresh.key in known:
+            return known[fresh.key]
+        self.specializations.append(fresh)
+        return fresh
 
     def drop_verified_inputs(self) -> None:
-        """Passing cases give up their input arrays (their sha256 stays);
-        failing cases keep theirs. Idempotent."""
+        """Passing cases give up their input arrays; failing ones keep them.
+        Safe to call more than once."""
         for spec in self.specializations:
-            for case, call in zip(spec.cases, spec.calls):
-                if case.passed and call is not None:
-                    call.inputs = {}
+            spec.release_passing_inputs()
 
 
 def by_family(evidences) -> dict:
+    """{kernel family: [its SpecializationEvidence across the gates]}, in
+    the order the families first appear."""
     families: dict = {}
-    for evidence in evidences:
-        for spec in evidence.specializations:
-            families.setdefault(spec.kernel, []).append(spec)
+    for spec in (s for ev in evidences for s in ev.specializations):
+        families.setdefault(spec.kernel, []).append(spec)
     return families
 
 
-def _case_line(case: CaseEvidence) -> str:
-    if case.err is None or case.tol is None:
-        verdict = "pass" if case.passed else f"FAIL: {case.detail or 'no verdict'}"
-        return f"{case.label}  {verdict}"
-    line = (f"{case.label}  err {case.err:9.3e}  tol {case.tol:9.3e}  "
-            f"{'pass' if case.passed else 'FAIL'}")
-    return line + (f"  ({case.detail})" if case.detail else "")
-
-
-def render_banner(evidence: GateEvidence, header: str, out=print) -> None:
-    """The gate's console banner, rendered from the evidence alone."""
-    out(header)
+def banner_lines(evidence: GateEvidence, header: str) -> Iterator[str]:
+    """The gate's console banner, line by line, from the evidence alone."""
+    yield header
     for check in evidence.checks:
-        out(f"  [check] {_case_line(check)}")
+        yield f"  check  {check.describe()}"
     for spec in evidence.specializations:
-        joined = " ".join(f"{k}={v}" for k, v in sorted(spec.template.items()))
-        out(f"  {spec.kernel} [{joined}] {spec.cases_passed}/{spec.cases_run} passed")
+        yield (f"  {spec.kernel} {{{spec.template_text}}}: "
+               f"{spec.cases_passed} of {spec.cases_run} cases ok")
         for case in spec.cases:
-            out(f"    {_case_line(case)}")
-    verdict = "green" if evidence.ok else "NOT GREEN"
-    out(f"  gate {evidence.gate}: {evidence.cases_passed}/{evidence.cases_run} cases, "
-        f"checks {'pass' if evidence.checks_passed else 'FAIL'} -> {verdict}")
+            yield f"      {case.describe()}"
+    status = "GREEN" if evidence.ok else "NOT GREEN"
+    checks = "ok" if evidence.checks_passed else "FAILED"
+    yield (f"  => {evidence.gate} {status}: {evidence.cases_passed} of {evidence.cases_run} "
+           f"cases ok, side checks {checks}")
+
+
+def render_banner(evidence: GateEvidence, header: str,
+                  out: Callable[[str], object] = print) -> None:
+    for line in banner_lines(evidence, header):
+        out(line)

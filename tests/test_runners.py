@@ -144,7 +144,7 @@ def test_no_device_is_unsupported_and_bad_cases_are_invalid(monkeypatch):
                   label="bad")
     res = runner.run_candidate([(spec, [good]), (spec, [bad])])
     assert res[0][0].status is RunStatus.UNSUPPORTED
-    assert res[1][0].status is RunStatus.INVALID_SPEC and "does not supply" in res[1][0].detail
+    assert res[1][0].status is RunStatus.INVALID_SPEC and "input 'x' is missing" in res[1][0].detail
 
 
 def test_launch_modes_round_trip():
@@ -163,3 +163,19 @@ def test_hiprtc_builds_candidates_and_reports_compile_errors():
     assert code[:4] == b"\x7fELF"
     with pytest.raises(rtc.CompileError, match="undeclared identifier"):
         rtc.compile_source('extern "C" __global__ void k(float* y) { y[0] = nothing_here; }')
+
+
+def test_specialize_reports_every_problem_and_keeps_escaped_dollars():
+    from kernelverify_amd.runners.specialize import placeholders
+
+    tmpl = KernelSpec(source="k<$T, ${N}> costs $$5 // $T again", entry_point="k_$T",
+                      bindings=(Binding(BindingKind.OUTPUT),), name="t")
+    assert placeholders(tmpl.source) == ["T", "N"]
+    spec = specialize(tmpl, {"T": "half", "N": 3})
+    assert spec.source == "k<half, 3> costs $5 // half again" and spec.entry_point == "k_half"
+    with pytest.raises(SpecError) as err:
+        specialize(tmpl, {"T": "half", "M": 1})
+    assert "$N" in str(err.value) and "['M']" in str(err.value)
+    bad = KernelSpec(source="x = $1", entry_point="k", bindings=(Binding(BindingKind.OUTPUT),))
+    with pytest.raises(SpecError):
+        specialize(bad, {})
