@@ -12,9 +12,15 @@ re-targeted to HIP):
   configuration);
 - weights rotate over >= 1 GiB of distinct artefact copies, more than the
   256 MB Infinity Cache, so every launch reads HBM;
-- W warmup launches, then EXACTLY K launches back-to-back on one stream,
-  bracketed by device synchronisation, timed by HIP events recorded on that
-  stream; ms_per_step = elapsed / K;
+- W warmup launches, then a HIP graph holding EXACTLY K launches
+  back-to-back on one stream, bracketed by event-record nodes inside the
+  graph (the host's graph-launch latency stays out of the window), replayed
+  for ROUNDS >= 7 rounds between device synchronisations; ms_per_step is the
+  median over rounds of elapsed / K, and ``timing`` carries every round's
+  min, max and max/min spread (a row over 1.5 is re-timed once, then
+  flagged, bench/interleave.py:48, :77-103). ``timing_5ms_samples`` repeats
+  the headline with rounds of at least 5 ms of launches (interleave.py:38)
+  as a cross-check; every other row is timed that way;
 - ``roofline.achieved`` = algorithmic bytes per launch / ms_per_step, with
   the bytes of ``kernelverify_amd.pack.wide_qmv.algorithmic_bytes``;
   ``roofline.frac`` is against the 8 TB/s spec and
@@ -281,14 +287,53 @@ class MoeWorkload:
         return worst
 
 
-def time_steps(workload, steps: int, warmup: int, graph: bool = True):
-    """ms per step over EXACTLY ``steps`` back-to-back launches.
+ROUNDS = 7          # replays of one K-launch graph per row (bench/interleave.py:38-103)
+SPREAD_LIMIT = 1.5  # max/min of a row's rounds above which the row is re-timed, then rejected
+MIN_SAMPLE_MS = 5.0  # the reference's floor for one timed sample (interleave.py:38)
 
-    With ``graph`` the launches are captured once into a HIP graph and
-    replayed, so the host's per-launch cost (ctypes, Python) cannot starve
-    the GPU: the figure is the device's own time per call, as a serving loop
-    that replays a captured decode step sees it. Without it, every launch is
-    a host call (the eager figure, reported beside it).
+
+class Timing:
+    """Rounds of one row: per-call ms of each replay of a graph of exactly
+    ``steps`` launches, timed by event-record nodes inside the graph."""
+
+    def __init__(self, steps: int, round_ms: list[float], in_graph: bool, retried: bool):
+        self.steps = steps
+        self.round_ms = round_ms
+        self.in_graph = in_graph
+        self.retried = retried
+
+    @property
+    def ms(self) -> float:
+        return float(np.median(self.round_ms))
+
+    @property
+    def spread(self) -> float:
+        return max(self.round_ms) / min(self.round_ms)
+
+    @property
+    def ok(self) -> bool:
+        return self.spread <= SPREAD_LIMIT
+
+    def summary(self) -> dict:
+        return {"rounds": len(self.round_ms), "launches_per_round": self.steps,
+                "median_us": round(self.ms * 1e3, 3),
+                "min_us": round(min(self.round_ms) * 1e3, 3),
+                "max_us": round(max(self.round_ms) * 1e3, 3),
+                "spread": round(self.spread, 4), "spread_ok": self.ok,
+                "events": "inside the graph" if self.in_graph else "around the graph launch"}
+
+
+def time_rounds(workload, steps: int, warmup: int, rounds: int = ROUNDS) -> Timing:
+    """ms per call: ``rounds`` replays of one HIP graph holding EXACTLY
+    ``steps`` back-to-back launches (the weights rotating over >= 1 GiB).
+
+    The start and stop events are event-record nodes inside the graph, so
+    the host's graph-launch latency is outside the window: each round is the
+    device's own time for ``steps`` calls, as a serving loop that replays a
+    captured decode step sees it. The value is the median over rounds; a row
+    whose max/min over rounds exceeds SPREAD_LIMIT is timed again once and
+    reported with ``spread_ok`` false if it still does (the reference's
+    reference-arm rule, bench/interleave.py:48, :77-103).
     """
     from kernelverify_amd import hip
 
@@ -296,32 +341,56 @@ def time_steps(workload, steps: int, warmup: int, graph: bool = True):
     for _ in range(warmup):
         workload.step(stream)
     hip.synchronize()
-    g = None
-    if graph:
-        g = hip.Graph(stream, lambda: [workload.step(stream) for _ in range(steps)])
-        g.launch()  # the replay itself warmed once
-        stream.synchronize()
-    hip.synchronize()
     start, stop = hip.Event(), hip.Event()
-    start.record(stream)
-    if g is not None:
-        g.launch()
-    else:
+
+    def body(external: bool):
+        (start.record_external if external else start.record)(stream)
         for _ in range(steps):
             workload.step(stream)
-    stop.record(stream)
-    stop.synchronize()
+        (stop.record_external if external else stop.record)(stream)
+
+    in_graph = True
+    try:
+        g = hip.Graph(stream, lambda: body(True))
+    except hip.HipError as exc:  # a runtime without event nodes: events around the launch
+        log(f"[bench] event nodes unavailable ({exc}); timing around the graph launch")
+        in_graph = False
+        g = hip.Graph(stream, lambda: [workload.step(stream) for _ in range(steps)])
+
+    def one_round() -> float:
+        if in_graph:
+            g.launch()
+        else:
+            start.record(stream)
+            g.launch()
+            stop.record(stream)
+        stream.synchronize()
+        return start.elapsed_ms(stop) / steps
+
+    one_round()  # the replay itself warmed once
     hip.synchronize()
-    if g is not None:
-        g.destroy()
-    return start.elapsed_ms(stop) / steps
+    t = Timing(steps, [one_round() for _ in range(rounds)], in_graph, False)
+    if not t.ok:
+        t = Timing(steps, [one_round() for _ in range(rounds)], in_graph, True)
+    hip.synchronize()
+    g.destroy()
+    return t
 
 
-def cpu_baseline(fn, budget_s: float = 12.0, min_reps: int = 3):
-    """Best and median wall time of the CPU path over a bounded sample."""
+def sample_steps(workload, warmup: int, floor: int) -> int:
+    """Launches per round for a secondary row: at least ``floor`` and at
+    least MIN_SAMPLE_MS of back-to-back launches (one short probe round)."""
+    probe = time_rounds(workload, 20, warmup, rounds=1)
+    return max(floor, int(np.ceil(MIN_SAMPLE_MS / max(probe.ms, 1e-6))))
+
+
+def cpu_baseline(fn, budget_s: float = 12.0, min_reps: int = 20):
+    """Best and median wall time of the CPU path: at least ``min_reps`` calls
+    (the reference found best-of-5 unstable on CPU), more while ``budget_s``
+    lasts, at most 50."""
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < 20):
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < 50):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
@@ -401,7 +470,7 @@ def blas_vendor() -> str:
 
 def cpu_row(workload, gpu_out, what: str) -> dict | None:
     """The CPU path of a KV or MoE row on the same inputs, a bounded sample
-    (about 4 s, at least 2 calls), after a check of its output against the
+    (at least 20 calls), after a check of its output against the
     verified GPU output; None (logged) if they disagree."""
     fn = workload.cpu_fn()
     ref = np.asarray(gpu_out, dtype=np.float64)
@@ -409,7 +478,7 @@ def cpu_row(workload, gpu_out, what: str) -> dict | None:
     if not np.max(np.abs(got - ref)) <= 4 * 9.77e-4 * np.max(np.abs(ref)):
         log(f"[bench] CPU path of {workload.name} disagrees with the GPU output; not timed")
         return None
-    best, med, n = cpu_baseline(fn, budget_s=4.0, min_reps=2)
+    best, med, n = cpu_baseline(fn, budget_s=4.0, min_reps=20)
     return {"us_per_call": round(best * 1e6, 1), "median_us": round(med * 1e6, 1),
             "GBps": round(workload.bytes / best / 1e9, 3), "calls": n, "cores": blas_threads(),
             "kind": "port", "path": what}
@@ -477,8 +546,13 @@ def main() -> int:
         print(f"bench.py: verification failed for {head.name}", file=sys.stderr)
         return 1
 
-    ms = time_steps(head, args.steps, args.warmup)
+    timing = time_rounds(head, args.steps, args.warmup)
+    ms = timing.ms
     us = ms * 1e3
+    log(f"[bench] {head.name} rounds: {timing.summary()}")
+    # the same kernel over samples of at least MIN_SAMPLE_MS, as a cross-check
+    # of the K-launch figure (not the value)
+    long = time_rounds(head, sample_steps(head, 0, args.steps), 0)
     gbs = head.bytes / (ms * 1e-3) / 1e9
     log(f"[bench] {head.name}: {us:.3f} us/call, {gbs:.1f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)")
 
@@ -487,11 +561,12 @@ def main() -> int:
     # ceiling as well as the spec).
     ceiling = None
     if not args.headline_only:
-        c_gbs, c_us = roofline.read_like(head.bytes)
+        c_gbs, c_us, c_shape = roofline.best_read_like(head.bytes)
         ceiling = {"GBps": round(c_gbs, 1), "us_per_launch": round(c_us, 3),
-                   "frac": round(gbs / c_gbs, 4),
-                   "probe": "kvp_probe_stream_read, back-to-back launches reading the same bytes "
-                            "per launch from a >= 1 GiB rotation (roofline.read_like)"}
+                   "frac": round(gbs / c_gbs, 4), "probe_shape": c_shape,
+                   "probe": "kvp_probe_read_tiled, back-to-back launches reading the same bytes "
+                            "per launch from a >= 1 GiB rotation, fastest of the sweep's leading "
+                            "shapes (roofline.best_read_like)"}
         log(f"[bench] measured read ceiling at {head.bytes} B/launch: {ceiling}")
 
     secondary = []
@@ -506,10 +581,12 @@ def main() -> int:
             if not e <= t:
                 log(f"[bench] verify FAILED {w.name}: {e:.3e} > {t:.3e}")
                 continue
-            ms2 = time_steps(w, max(200, args.steps // 2), args.warmup)
+            t2 = time_rounds(w, sample_steps(w, args.warmup, max(200, args.steps // 2)), 0)
+            ms2 = t2.ms
             secondary.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3),
                               "GBps": round(w.bytes / (ms2 * 1e-3) / 1e9, 1),
-                              "frac_8TBps": round(w.bytes / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+                              "frac_8TBps": round(w.bytes / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                              "timing": t2.summary()})
             log(f"[bench] {secondary[-1]}")
             del w
 
@@ -523,12 +600,13 @@ def main() -> int:
         if not ratio <= 1.0:
             log(f"[bench] verify FAILED {w.name}: error {ratio:.2f} x bound")
             continue
-        ms2 = time_steps(w, max(200, args.steps // 2), args.warmup)
+        t2 = time_rounds(w, sample_steps(w, args.warmup, max(200, args.steps // 2)), 0)
+        ms2 = t2.ms
         gbs2 = w.bytes / (ms2 * 1e-3) / 1e9
         kv.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3), "GBps": round(gbs2, 1),
                    "frac_8TBps": round(gbs2 / PEAK_HBM_GBS, 4), "bytes": w.bytes,
-                   "verify_err_over_bound": round(ratio, 4)})
-        kv[-1]["frac_measured_ceiling"] = round(gbs2 / roofline.read_like(w.bytes)[0], 4)
+                   "verify_err_over_bound": round(ratio, 4), "timing": t2.summary()})
+        kv[-1]["frac_measured_ceiling"] = round(gbs2 / roofline.best_read_like(w.bytes)[0], 4)
         if not args.no_cpu:
             kv[-1]["cpu"] = cpu_row(w, got, "dequantize the stored caches, fp32 scores, "
                                     "softmax over T + 1, values (native_kernels.py:168-221)")
@@ -543,13 +621,14 @@ def main() -> int:
         if not ratio <= 1.0:
             log(f"[bench] verify FAILED {w.name}: error {ratio:.2f} x bound")
             continue
-        ms3 = time_steps(w, max(200, args.steps // 4), args.warmup)
+        t3 = time_rounds(w, sample_steps(w, args.warmup, max(100, args.steps // 4)), 0)
+        ms3 = t3.ms
         gbs3 = w.bytes / (ms3 * 1e-3) / 1e9
         moe_rows.append({"workload": w.name, "us_per_call": round(ms3 * 1e3, 3),
                          "GBps": round(gbs3, 1), "frac_8TBps": round(gbs3 / PEAK_HBM_GBS, 4),
                          "unique_experts": w.unique, "bytes": w.bytes,
-                         "verify_err_over_bound": round(ratio, 4)})
-        moe_rows[-1]["frac_measured_ceiling"] = round(gbs3 / roofline.read_like(w.bytes)[0], 4)
+                         "verify_err_over_bound": round(ratio, 4), "timing": t3.summary()})
+        moe_rows[-1]["frac_measured_ceiling"] = round(gbs3 / roofline.best_read_like(w.bytes)[0], 4)
         if not args.no_cpu:
             moe_rows[-1]["cpu"] = cpu_row(w, got, "softmax top-8 routing, each routed expert's "
                                           "gate/up/down dequantized once, fp32 SwiGLU "
@@ -581,7 +660,8 @@ def main() -> int:
     line = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
-        "us_per_call": round(us, 3), "higher_is_better": True, "scaling": "weak",
+        "us_per_call": round(us, 3), "timing": timing.summary(),
+        "timing_5ms_samples": long.summary(), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "u4 codes x f16 -> f32 accumulate",
         "data": "synthetic (BASELINE configs[1] distributions, seed 0)",
         "config": {"workload": head.name, "d_out": 14336, "d_in": 4096, "bits": 4, "group": 64,

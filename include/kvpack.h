@@ -191,6 +191,22 @@ int kvp_probe_stream_read(const void* src, size_t n_bytes, float* read_sink, int
 int kvp_probe_stream_copy(const void* src, void* dst, size_t n_bytes, int blocks,
                           void* stream);
 
+/* Tunable read probe (the sweep behind the measured ceiling). Each block
+ * reads whole tiles of threads x unroll 16-byte units, every lane's `unroll`
+ * loads issued before any is used; flags bits 0-1 pick the load (0 plain,
+ * 1 non-temporal, 2 buffer), bit 2 gives each block one contiguous range of
+ * tiles instead of grid-strided tiles. threads in {64, 128, 256, 512, 1024},
+ * unroll in {1, 2, 4, 8, 16}; `sink` receives one float per block. */
+int kvp_probe_read_tiled(const void* src, size_t n_bytes, float* sink, int blocks, int threads,
+                         int unroll, int flags, void* stream);
+
+/* Compute-ceiling probes (replaces bench/metal/roofline_probe.mm:103-144, the
+ * fp32 / fp16 FMA peaks): kind 0 fp32 FMA, 1 V_DOT2_F32_F16, 2
+ * V_MFMA_F32_16X16X32_F16, in 256-thread blocks of independent chains.
+ * kvp_probe_compute_flops gives the flops one launch performs. */
+double kvp_probe_compute_flops(int kind, int blocks, int iters);
+int kvp_probe_compute(int kind, int blocks, int iters, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

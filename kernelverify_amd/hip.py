@@ -55,7 +55,9 @@ def runtime() -> ctypes.CDLL:
         "hipEventCreate": [ctypes.POINTER(vp)],
         "hipEventDestroy": [vp],
         "hipEventRecord": [vp, vp],
+        "hipEventRecordWithFlags": [vp, vp, ctypes.c_uint],
         "hipEventSynchronize": [vp],
+        "hipEventQuery": [vp],
         "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp],
         "hipGetLastError": [],
         "hipMemGetInfo": [ctypes.POINTER(sz), ctypes.POINTER(sz)],
@@ -220,8 +222,36 @@ class Event:
         s = ctypes.c_void_p(stream.handle if stream else None)
         check(runtime().hipEventRecord(ctypes.c_void_p(self.handle), s), "hipEventRecord")
 
+    def record_external(self, stream: Stream) -> None:
+        """Record on ``stream``; under stream capture this becomes an event
+        record node of the graph (hipEventRecordExternal), so a replay
+        stamps the event on the device between the nodes around it."""
+        check(runtime().hipEventRecordWithFlags(ctypes.c_void_p(self.handle),
+                                                ctypes.c_void_p(stream.handle),
+                                                HIP_EVENT_RECORD_EXTERNAL),
+              "hipEventRecordWithFlags")
+
     def synchronize(self) -> None:
         check(runtime().hipEventSynchronize(ctypes.c_void_p(self.handle)), "hipEventSynchronize")
+
+    def query(self) -> bool:
+        """True once the work before the record has completed (no wait)."""
+        err = runtime().hipEventQuery(ctypes.c_void_p(self.handle))
+        if err == HIP_ERROR_NOT_READY:
+            return False
+        check(err, "hipEventQuery")
+        return True
+
+    def wait_until(self, deadline: float, poll_s: float = 2e-4) -> bool:
+        """Poll until the event completes or the host clock
+        (``time.perf_counter``) passes ``deadline``; True if it completed."""
+        import time
+
+        while not self.query():
+            if time.perf_counter() > deadline:
+                return False
+            time.sleep(poll_s)
+        return True
 
     def elapsed_ms(self, later: "Event") -> float:
         ms = ctypes.c_float()
@@ -238,6 +268,8 @@ class Event:
 
 
 HIP_STREAM_CAPTURE_RELAXED = 2
+HIP_EVENT_RECORD_EXTERNAL = 1
+HIP_ERROR_NOT_READY = 600
 
 
 class Graph:

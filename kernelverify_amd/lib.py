@@ -69,6 +69,9 @@ SIGNATURES = {
     "kvp_moe_swiglu": (_i, [_vp] * 13 + [_i] * 7 + [_vp, _sz, _vp]),
     "kvp_probe_stream_read": (_i, [_vp, _sz, _vp, _i, _vp]),
     "kvp_probe_stream_copy": (_i, [_vp, _vp, _sz, _i, _vp]),
+    "kvp_probe_read_tiled": (_i, [_vp, _sz, _vp, _i, _i, _i, _i, _vp]),
+    "kvp_probe_compute_flops": (ctypes.c_double, [_i, _i, _i]),
+    "kvp_probe_compute": (_i, [_i, _i, _i, _vp, _vp]),
 }
 
 
