@@ -108,9 +108,21 @@ class RoutedLinear(nn.Module):
             return "bias-term"
         if x.dtype != torch.float16 or inner.scales.dtype != torch.float16:
             return f"dtype-{x.dtype}-{inner.scales.dtype}"
+        if inner.biases.dtype != torch.float16:
+            return f"biases-dtype-{inner.biases.dtype}"
         d_in = x.shape[-1]
         if d_in % GROUP or d_in != inner.d_in:
             return f"din-{d_in}"
+        # the kernel reads these buffers raw: (d_out, d_in * bits / 32) words
+        # and (d_out, d_in / 64) scales and biases, densely packed
+        words = d_in * inner.bits // 32
+        if (inner.weight.dim() != 2 or tuple(inner.weight.shape) != (inner.d_out, words)
+                or inner.weight.element_size() != 4):
+            return f"weight-shape-{tuple(inner.weight.shape)}"
+        if tuple(inner.biases.shape) != tuple(inner.scales.shape):
+            return f"biases-shape-{tuple(inner.biases.shape)}"
+        if not all(t.is_contiguous() for t in (inner.weight, inner.scales, inner.biases)):
+            return "noncontiguous"
         m = x.numel() // d_in
         if not wide_qmv.should_dispatch(m, inner.bits, inner.d_out, d_in):
             return f"m-{m}-outside-dispatch-{inner.d_out}x{d_in}"

@@ -83,6 +83,30 @@ def test_every_refusal_names_its_reason():
         assert RoutedLinear(other, Patch(nn.Module())).ineligible(x) == why
 
 
+def test_buffers_the_kernel_would_misread_are_named_refusals():
+    """The kernel reads weight, scales and biases raw: a biases dtype other
+    than fp16, a code array of the wrong shape (a short one would be read
+    past its end) or a strided buffer is refused by name, before M."""
+    layer, art = _layer(128, 256, 4)
+    x = torch.zeros((1, 256), dtype=torch.float16)
+    w, s, b = layer.weight, layer.scales, layer.biases
+
+    def why(weight, scales, biases):
+        return RoutedLinear(QuantizedLinear(weight, scales, biases, 4),
+                            Patch(nn.Module())).ineligible(x)
+
+    assert why(w, s, b.float()) == "biases-dtype-torch.float32"
+    assert why(w, s, b.to(torch.bfloat16)) == "biases-dtype-torch.bfloat16"
+    assert why(w[:, :16].contiguous(), s, b) == "weight-shape-(128, 16)"
+    assert why(w[:64], s, b) == "weight-shape-(64, 32)"
+    assert why(w, s, b[:, :2].contiguous()) == "biases-shape-(128, 2)"
+    strided = torch.zeros((128, 64), dtype=torch.int32)[:, ::2]
+    strided.copy_(w)
+    assert why(strided, s, b) == "noncontiguous"
+    assert why(w, s.t().contiguous().t(), b) == "noncontiguous"
+    assert why(w, s, b) == "m-1-outside-dispatch-128x256"
+
+
 def test_patch_wraps_every_site_counts_and_restores():
     a, _ = _layer(4096, 4096, 4, seed=1)
     b, _ = _layer(128, 256, 4, seed=2)
