@@ -125,6 +125,25 @@ int kvp_kv_decode(const void* q, const uint32_t* k_wq, const void* k_scales,
                   int n_kv_heads, int head_dim, int t_stride, int bits, int cache_per_sequence,
                   int chunk, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of kvp_kv_decode. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results as kvp_kv_decode without the workspace: the split
+ * partials live in a fixed static device array of
+ * kvp_kv_decode_static_scratch_bytes() bytes (4 MiB) per GPU, held until the
+ * process ends. A call whose kvp_kv_decode_workspace_bytes(...) exceeds that
+ * is refused with KVP_INVALID. Nothing is allocated and nothing is cleared:
+ * every partial a call reads is written by the same call. Every call on one
+ * GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams at once) race; order them on one stream. */
+size_t kvp_kv_decode_static_scratch_bytes(void);
+int kvp_kv_decode_static(const void* q, const uint32_t* k_wq, const void* k_scales,
+                         const void* k_biases, const uint32_t* v_wq, const void* v_scales,
+                         const void* v_biases, const void* new_k, const void* new_v,
+                         const int32_t* t_cached, void* out, int out_dtype, int batch,
+                         int n_heads, int n_kv_heads, int head_dim, int t_stride, int bits,
+                         int cache_per_sequence, int chunk, void* stream);
+
 /* ------------------------------------------------------------------------
  * MoE routing: softmax over all n_experts, top-k BY PROBABILITY with ties
  * to the lower expert index, gates renormalised over the k chosen.

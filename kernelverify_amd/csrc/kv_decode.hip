@@ -41,6 +41,7 @@
 // (p * s) * q + p * b in fp32.
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1101,6 +1102,46 @@ int launch_bits(int dh, int G, const KvArgs& a, int batch, hipStream_t st) {
   return launch_dh<BITS, 128>(G, a, batch, st);
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (kvp_kv_decode_static): the
+// split partials of one call live in this fixed device array instead of a
+// caller workspace. Every GPU the library runs on holds its own copy until
+// the process ends. In host code `scratch` names a host-side stand-in, never
+// device memory: the device address comes from hipGetSymbolAddress, taken
+// once per device with that device current, and only that address is passed
+// to kernels. Nothing in it must start at zero (every partial a call reads
+// is written by the same call), and calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+constexpr size_t kStaticScratchBytes = size_t(4) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on first use.
+int static_scratch(void** ptr) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return set_error(KVP_NO_DEVICE, "kvp_kv_decode_static: hipGetDevice: %s",
+                     hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(KVP_UNSUPPORTED, "kvp_kv_decode_static: device %d beyond %d", dev,
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return set_error(KVP_LAUNCH_ERROR, "kvp_kv_decode_static: hipGetSymbolAddress: %s",
+                       hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return KVP_OK;
+}
+
 }  // namespace
 }  // namespace kvp
 
@@ -1176,4 +1217,38 @@ extern "C" int kvp_kv_decode(const void* q, const uint32_t* k_wq, const void* k_
     case 4: return launch_bits<4>(head_dim, G, a, batch, st);
     default: return launch_bits<8>(head_dim, G, a, batch, st);
   }
+}
+
+extern "C" size_t kvp_kv_decode_static_scratch_bytes(void) { return kvp::kStaticScratchBytes; }
+
+extern "C" int kvp_kv_decode_static(const void* q, const uint32_t* k_wq, const void* k_scales,
+                                    const void* k_biases, const uint32_t* v_wq,
+                                    const void* v_scales, const void* v_biases,
+                                    const void* new_k, const void* new_v,
+                                    const int32_t* t_cached, void* out, int out_dtype,
+                                    int batch, int n_heads, int n_kv_heads, int head_dim,
+                                    int t_stride, int bits, int cache_per_sequence, int chunk,
+                                    void* stream) {
+  using namespace kvp;
+  clear_error();
+  // The chunk decides the scratch size, so resolve it first (the checks it
+  // needs); kvp_kv_decode checks every argument again.
+  KVP_REQUIRE(batch >= 1 && n_heads >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0,
+              "kvp_kv_decode_static: batch=%d n_heads=%d n_kv_heads=%d", batch, n_heads,
+              n_kv_heads);
+  KVP_REQUIRE(t_stride >= 0, "kvp_kv_decode_static: t_stride=%d", t_stride);
+  if (chunk <= 0) chunk = pick_chunk(bits, batch, n_kv_heads, t_stride, n_heads / n_kv_heads);
+  KVP_REQUIRE(chunk % 64 == 0 && chunk >= 64, "kvp_kv_decode_static: chunk=%d (a multiple of 64)",
+              chunk);
+  const size_t need = kvp_kv_decode_workspace_bytes(batch, n_heads, head_dim, t_stride, chunk);
+  KVP_REQUIRE(need <= kStaticScratchBytes,
+              "kvp_kv_decode_static: this call needs %zu bytes of scratch; the static scratch "
+              "holds %zu (fewer sequences or heads, or a longer chunk)",
+              need, kStaticScratchBytes);
+  void* ws = nullptr;
+  const int rc = static_scratch(&ws);
+  if (rc != KVP_OK) return rc;
+  return kvp_kv_decode(q, k_wq, k_scales, k_biases, v_wq, v_scales, v_biases, new_k, new_v,
+                       t_cached, out, out_dtype, batch, n_heads, n_kv_heads, head_dim, t_stride,
+                       bits, cache_per_sequence, chunk, ws, kStaticScratchBytes, stream);
 }

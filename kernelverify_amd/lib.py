@@ -61,6 +61,8 @@ SIGNATURES = {
     "kvp_qmv": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "kvp_kv_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "kvp_kv_decode": (_i, [_vp] * 11 + [_i] * 9 + [_vp, _sz, _vp]),
+    "kvp_kv_decode_static_scratch_bytes": (_sz, []),
+    "kvp_kv_decode_static": (_i, [_vp] * 11 + [_i] * 9 + [_vp]),
     "kvp_moe_route": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "kvp_moe_route_logits": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "kvp_moe_permute": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
