@@ -23,8 +23,14 @@
  *     (code i at bits [i*bits, (i+1)*bits)), plus fp16 scale and bias per
  *     64-code group; the dequantized value is scale * q + bias.
  *   - fp16 arguments are IEEE binary16 (`void*`, 2 bytes per element).
- *   - Every intermediate is binary32 or wider; outputs are rounded to their
- *     storage dtype once (kernelverify/tolerance/contract.py:23-30, C1).
+ *   - Accumulation is binary32 throughout and outputs are rounded to their
+ *     storage dtype once (kernelverify/tolerance/contract.py:23-30, C1),
+ *     with two stated exceptions where an fp32 intermediate enters the
+ *     matrix cores as an fp16 hi + lo pair, about 22 significant bits (the
+ *     products are exact, the sums fp32): the probability-scaled value
+ *     weight p * scale of kvp_kv_decode's value side at 4 and 8 bits, and
+ *     the SwiGLU hidden state entering kvp_moe_swiglu's down projection at
+ *     4 and 8 bits. Every other intermediate is binary32 or wider.
  */
 #ifndef KVPACK_H_
 #define KVPACK_H_
@@ -174,7 +180,8 @@ int kvp_moe_permute(const uint32_t* idx, int32_t* offsets, int32_t* perm, int n,
  * Replaces `kv_moe_dispatch` (kernelverify/pack/moe_dispatch.py:84-138).
  *   x fp16 [n][d_in]; w_q uint32 [n_experts][d_out][d_in * bits / 32];
  *   scales, biases fp16 [n_experts][d_out][d_in / 64]; out [n][d_out].
- * bits in {2, 3, 4, 8}; k <= 32. */
+ * A slot naming no expert (idx >= n_experts) adds nothing, as in
+ * kvp_moe_swiglu. bits in {2, 3, 4, 8}; k <= 32. */
 int kvp_moe_dispatch(const void* x, const uint32_t* idx, const float* gate,
                      const uint32_t* w_q, const void* scales, const void* biases, void* out,
                      int out_dtype, int n, int k, int n_experts, int d_out, int d_in, int bits,
@@ -201,6 +208,17 @@ int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* gate,
                    const uint32_t* down_wq, const void* down_scales, const void* down_biases,
                    void* out, int out_dtype, int n, int k, int n_experts, int d_model,
                    int d_ffn, int bits, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Kernel-selection overrides, for tiling sweeps and A/B tests only: the
+ * library's own choice applies to every key that is not set, and nothing
+ * else (no environment variable) changes which kernel a call runs. Keys:
+ * "qmv_path" (1 streaming, 2 resident, 3 chunked, 4 matrix cores,
+ * 5 persistent), "qmv_per_cu", "qmv_blocks", "qmv_kw", "qmv_rw",
+ * "qmv_mfma_tiles", "moe_valu", "moe_kq", "moe_permute". value -1 restores
+ * the library's choice. Process-wide; set before the calls it should
+ * affect. No counterpart in the reference (its kernels have one body). */
+int kvp_set_tuning(const char* key, int value);
+int kvp_get_tuning(const char* key, int* value);
 
 /* HBM roofline probe kernels (replaces bench/metal/roofline_probe.mm:35-144
  * stream_read / stream_copy). `n_bytes` multiple of 16. read_sink receives a

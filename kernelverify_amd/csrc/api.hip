@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <string>
 
 #include "common.h"
@@ -31,6 +32,25 @@ int set_error(int status, const char* fmt, ...) {
 void clear_error() {
   g_last_error.clear();
   (void)hipGetLastError();
+}
+
+namespace {
+// Each slot holds value + 1; 0 (static zero-initialisation) means unset.
+std::atomic<int> g_tuning[kTuneCount];
+constexpr const char* kTuneNames[kTuneCount] = {
+    "qmv_path", "qmv_per_cu", "qmv_blocks", "qmv_kw", "qmv_rw", "qmv_mfma_tiles",
+    "moe_valu", "moe_kq", "moe_permute"};
+
+int tuning_index(const char* key) {
+  for (int i = 0; key && i < kTuneCount; ++i)
+    if (strcmp(key, kTuneNames[i]) == 0) return i;
+  return -1;
+}
+}  // namespace
+
+int tuning(TuneKey key, int fallback) {
+  const int v = g_tuning[key].load(std::memory_order_relaxed);
+  return v == 0 ? fallback : v - 1;
 }
 
 int check_launch(const char* what) {
@@ -122,6 +142,23 @@ int kvp_device_info(int device, char* name, size_t name_cap, char* arch, size_t 
     return kvp::set_error(KVP_NO_DEVICE, "kvp_device_info: device %d is %s, not gfx950", device,
                           p.gcnArchName);
   }
+  return KVP_OK;
+}
+
+int kvp_set_tuning(const char* key, int value) {
+  kvp::clear_error();
+  const int i = kvp::tuning_index(key);
+  KVP_REQUIRE(i >= 0, "kvp_set_tuning: unknown key %s", key ? key : "(null)");
+  KVP_REQUIRE(value >= -1, "kvp_set_tuning: value %d (-1 restores the library's choice)", value);
+  kvp::g_tuning[i].store(value < 0 ? 0 : value + 1, std::memory_order_relaxed);
+  return KVP_OK;
+}
+
+int kvp_get_tuning(const char* key, int* value) {
+  kvp::clear_error();
+  const int i = kvp::tuning_index(key);
+  KVP_REQUIRE(i >= 0 && value, "kvp_get_tuning: unknown key %s", key ? key : "(null)");
+  *value = kvp::tuning(static_cast<kvp::TuneKey>(i), -1);
   return KVP_OK;
 }
 

@@ -34,6 +34,24 @@ void clear_error();
 // KVP_LAUNCH_ERROR with the runtime's own message.
 int check_launch(const char* what);
 
+// Kernel-selection overrides set through kvp_set_tuning (include/kvpack.h):
+// tuning(key, fallback) is the caller's value when one is set, else the
+// library's own choice `fallback`. Nothing else (no environment variable)
+// changes which kernel a call runs.
+enum TuneKey {
+  kTuneQmvPath,        // 1 streaming, 2 resident, 3 chunked, 4 matrix cores, 5 persistent
+  kTuneQmvPerCu,       // persistent M = 1 kernel: blocks per CU
+  kTuneQmvBlocks,      // resident kernel: grid size
+  kTuneQmvKw,          // chunked kernel: waves per row (1, 2, 4)
+  kTuneQmvRw,          // M <= 2 VALU kernels: rows per wave (2 or 4)
+  kTuneQmvMfmaTiles,   // matrix-core qmv: 16-row tiles per block (1, 2, 4)
+  kTuneMoeValu,        // 1: MoE experts on the VALU kernels
+  kTuneMoeKq,          // matrix-core experts: 1 tile per wave, or 4 waves per tile
+  kTuneMoePermute,     // 1: the separate permute launch even where in-block routing applies
+  kTuneCount
+};
+int tuning(TuneKey key, int fallback);
+
 // ---------------------------------------------------------------------------
 // Device side
 // ---------------------------------------------------------------------------

@@ -887,7 +887,8 @@ __global__ __launch_bounds__(kBlock) void dispatch_kernel(const f16* __restrict_
   stage_tokens<BITS, 1>(x, tok, 1, d_in, xs, xsum);
   float total[kRW] = {};
   for (int s = 0; s < k; ++s) {
-    const uint32_t e = min(idx[(size_t)t * k + s], (uint32_t)(n_experts - 1));
+    const uint32_t e = idx[(size_t)t * k + s];
+    if (e >= (uint32_t)n_experts) continue;  // names no expert: adds nothing (block-uniform)
     const float g = gate[(size_t)t * k + s];
     int rows[kRW];
 #pragma unroll
@@ -955,10 +956,10 @@ int check_route_args(int n, int n_experts, int k) {
 }
 
 // Matrix cores take the experts at 4 and 8 bits: four groups per step, at
-// most 16 steps (d_in <= 4096). KVP_MOE_VALU forces the VALU kernels.
+// most 16 steps (d_in <= 4096). Tuning key moe_valu = 1 forces the VALU kernels.
 bool mfma_experts(int bits, int d_in) {
   const int G = d_in / 64;
-  return (bits == 4 || bits == 8) && G % 4 == 0 && G <= 64 && getenv("KVP_MOE_VALU") == nullptr;
+  return (bits == 4 || bits == 8) && G % 4 == 0 && G <= 64 && tuning(kTuneMoeValu, 0) == 0;
 }
 
 // a.idx set: the gate/up launch routes in-block (matrix-core path only).
@@ -977,9 +978,9 @@ int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f3
       // (their x staging then spreads over four tiles; 2048-code rows,
       // measured: n = 8 61.2 against 62.0 us, n = 32 114.3 against 118.0);
       // four waves per tile for long rows of a few experts (n = 1: 27.4
-      // against 32.2 us). KVP_MOE_KQ (1 or 4) overrides for tiling sweeps.
-      const char* kq_env = getenv("KVP_MOE_KQ");
-      const bool short_rows = kq_env ? atoi(kq_env) == 1 : (G / 4 <= 4 || max_active >= 32);
+      // against 32.2 us). Tuning key moe_kq (1 or 4) overrides for tiling sweeps.
+      const int kq = tuning(kTuneMoeKq, (G / 4 <= 4 || max_active >= 32) ? 1 : 4);
+      const bool short_rows = kq == 1;
       const dim3 grid(short_rows ? (tiles + 3) / 4 : tiles, max_active);
 #define KVP_EXPERT(SW, F32, KQ, RT)                                                           \
   hipLaunchKernelGGL((expert_mfma_kernel<BITS, SW, F32, KQ, RT>), grid, dim3(kBlock), lds, st, a)
@@ -1161,9 +1162,9 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
   float* y = reinterpret_cast<float*>(ws + L.y);
   const int pairs = n * k;
   // A few pairs on the matrix-core path: the gate/up launch builds the
-  // permutation in-block (KVP_MOE_PERMUTE forces the permute launch).
+  // permutation in-block (tuning key moe_permute = 1 forces the permute launch).
   const bool route_in_block = pairs <= kFusedPairs && mfma_experts(bits, d_model) &&
-                              getenv("KVP_MOE_PERMUTE") == nullptr;
+                              tuning(kTuneMoePermute, 0) == 0;
   if (!route_in_block) {
     hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, st, idx, offsets, perm, active,
                        slot_of, pairs, n_experts);

@@ -763,11 +763,6 @@ size_t resident_lds_bytes(int d_in) {
   return units * (size_t)(M * G::kUnitPairs + M) * 4;
 }
 
-int env_int(const char* name, int fallback) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : fallback;
-}
-
 template <int BITS, int M, int RW, typename OutT>
 int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void* biases,
                void* out, int d_out, int d_in, hipStream_t stream) {
@@ -776,26 +771,29 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
   const size_t res_lds = resident_lds_bytes<BITS, M>(d_in);
   // Path: 1 streaming (no LDS; M <= 2), 2 resident x, 3 chunked x. Auto
   // (measured on MI355X): streaming for M = 1 except tall 4-bit matrices of
-  // short rows (below), resident when x fits, else chunked. KVP_QMV_PATH
-  // overrides for tiling sweeps.
+  // short rows (below), resident when x fits, else chunked. The tuning
+  // key qmv_path overrides for tiling sweeps.
   // Tall 4-bit M = 1 with rows of at most 4096 codes: x resident in LDS at
   // four blocks per CU (an equal share on every CU; 3.5 or 6 per CU lose),
   // two rows per wave. Measured against streaming: 14336 x 4096 8.46 / 8.85
   // us, 9728 x 2560 6.07 / 6.88, 8192 x 4096 6.15 / 6.41; 4096 x 4096 stays
   // streaming (5.07 / 4.47).
   const bool tall = M == 1 && BITS == 4 && d_in <= 4096 && d_out >= 8192;
-  int path = env_int("KVP_QMV_PATH", 0);
+  int path = tuning(kTuneQmvPath, 0);
   if (path == 0) path = (M == 1 && !tall) ? 1 : (res_lds <= kResidentLdsMax ? 2 : 3);
   if constexpr (M == 1 && G::kMagic) {
     const int upl = (units + kWave - 1) / kWave;
+    // its buffer descriptors and offsets are 32-bit, with 2^31 as the
+    // out-of-range sentinel: the code array must stay below 2 GiB
+    const bool persist_fits = (size_t)d_out * d_in / 8 * BITS < (size_t(1) << 31);
     // Persistent waves pay off when each has many row sets to walk: very
     // tall matrices (measured: 151936 x 2560 at 4 bits, 51.5 against 68.7 us).
-    if ((path == 5 || (path == 0 && d_out >= 65536)) && upl <= 4) {
+    if (persist_fits && (path == 5 || (path == 0 && d_out >= 65536)) && upl <= 4) {
       int dev = 0, cus = 0;
       hipGetDevice(&dev);
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
       const int sets = (d_out + 1) / 2;
-      int blocks = cus * env_int("KVP_QMV_PER_CU", 2);
+      int blocks = cus * tuning(kTuneQmvPerCu, 2);
       blocks = min(blocks, (sets + kWavesPerBlock - 1) / kWavesPerBlock);
 #define KVP_PERSIST(U)                                                                         \
   if (upl <= U) {                                                                              \
@@ -846,8 +844,8 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
       blocks = min(blocks, 4 * cus);
     }
-    blocks = env_int("KVP_QMV_BLOCKS", blocks);
-    if (blocks < 1) return set_error(KVP_INVALID, "kvp_qmv: KVP_QMV_BLOCKS=%d", blocks);
+    blocks = tuning(kTuneQmvBlocks, blocks);
+    if (blocks < 1) return set_error(KVP_INVALID, "kvp_qmv: tuning qmv_blocks=%d", blocks);
     hipLaunchKernelGGL((qmv_resident_kernel<BITS, M, RW, OutT>), dim3(blocks), dim3(kBlock),
                        res_lds, stream, static_cast<const f16*>(x), wq,
                        static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases),
@@ -867,8 +865,8 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
   const int row_waves = (d_out + RW - 1) / RW;
   int kw = 1;
   while (kw < kWavesPerBlock && row_waves * kw < 4096 && 2 * kw * kUPL <= rounds) kw *= 2;
-  kw = env_int("KVP_QMV_KW", kw);
-  if (kw != 1 && kw != 2 && kw != 4) return set_error(KVP_INVALID, "kvp_qmv: KVP_QMV_KW=%d", kw);
+  kw = tuning(kTuneQmvKw, kw);
+  if (kw != 1 && kw != 2 && kw != 4) return set_error(KVP_INVALID, "kvp_qmv: tuning qmv_kw=%d", kw);
   const size_t lds = (size_t)chunk_units * words_per_unit * 4;
   const int rows_per_block = (kWavesPerBlock / kw) * RW;
   const int blocks = (d_out + rows_per_block - 1) / rows_per_block;
@@ -880,15 +878,15 @@ int launch_qmv(const void* x, const uint32_t* wq, const void* scales, const void
 }
 
 // Rows per wave: the VGPR budget of RW * M accumulators. M <= 2 can run
-// RW = 2 or 4 (KVP_QMV_RW picks for tiling sweeps); wider M steps down.
+// RW = 2 or 4 (tuning key qmv_rw picks for tiling sweeps); wider M steps down.
 template <int BITS, int M, typename OutT>
 int launch_qmv_rw(const void* x, const uint32_t* wq, const void* scales, const void* biases,
                   void* out, int d_out, int d_in, hipStream_t stream) {
   if constexpr (M <= 2) {
-    // Two rows per wave; four (KVP_QMV_RW=4) halve the activation work per
+    // Two rows per wave; four (qmv_rw = 4) halve the activation work per
     // row of the streaming kernel, which measured faster only where the
     // resident kernel now serves (tall 4-bit M = 1 rows of <= 4096 codes).
-    if (env_int("KVP_QMV_RW", 2) == 4)
+    if (tuning(kTuneQmvRw, 2) == 4)
       return launch_qmv<BITS, M, 4, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
     return launch_qmv<BITS, M, 2, OutT>(x, wq, scales, biases, out, d_out, d_in, stream);
   } else {
@@ -914,8 +912,8 @@ template <typename OutT>
 int dispatch_bits(int bits, int m, const void* x, const uint32_t* wq, const void* s,
                   const void* b, void* out, int d_out, int d_in, hipStream_t st) {
   // Matrix cores for 4/8-bit at M >= 2 (qmv_mfma.hip): their cost does not
-  // grow with M. KVP_QMV_PATH=4 forces them at M = 1, 1..3 the VALU paths.
-  const int path = env_int("KVP_QMV_PATH", 0);
+  // grow with M. qmv_path = 4 forces them at M = 1, 1..3 the VALU paths.
+  const int path = tuning(kTuneQmvPath, 0);
   const bool fits = (size_t)d_out * d_in / 8 * bits < (size_t(1) << 31);  // 32-bit buffer offsets
   if ((bits == 4 || bits == 8) && fits && ((path == 0 && m >= 2) || path == 4))
     return launch_qmv_mfma(bits, sizeof(OutT) == 4, x, wq, s, b, out, m, d_out, d_in, st);

@@ -34,11 +34,6 @@ namespace {
 
 constexpr int kMfmaStageBytes = 64 * 1024;  // x chunk budget per block
 
-int env_int(const char* name, int fallback) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : fallback;
-}
-
 template <int BITS, int MT>
 struct MfmaStep {
   uint32_t w[MfmaShape<BITS, MT>::kWPL];
@@ -266,7 +261,7 @@ int launch_tiles(const void* x, const uint32_t* wq, const void* s, const void* b
   int pick = 1;
   if (tiles < 4096 && (tiles >= 768 || (tiles >= 512 && m >= 8))) pick = 4;
   else if (tiles >= 4096 && m >= 8) pick = 2;
-  const int v = env_int("KVP_QMV_MFMA_TILES", pick);
+  const int v = tuning(kTuneQmvMfmaTiles, pick);
   if (v == 4) return launch_mt<BITS, MT, 4, 4, OutT>(x, wq, s, b, out, m, d_out, d_in, st);
   if (v == 2) return launch_mt<BITS, MT, 2, 4, OutT>(x, wq, s, b, out, m, d_out, d_in, st);
   if (tiles >= 512) return launch_mt<BITS, MT, 1, 4, OutT>(x, wq, s, b, out, m, d_out, d_in, st);

@@ -69,6 +69,8 @@ SIGNATURES = {
     "kvp_moe_dispatch": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
     "kvp_moe_swiglu_workspace_bytes": (_sz, [_i] * 5),
     "kvp_moe_swiglu": (_i, [_vp] * 13 + [_i] * 7 + [_vp, _sz, _vp]),
+    "kvp_set_tuning": (_i, [_cp, _i]),
+    "kvp_get_tuning": (_i, [_cp, _ip]),
     "kvp_probe_stream_read": (_i, [_vp, _sz, _vp, _i, _vp]),
     "kvp_probe_stream_copy": (_i, [_vp, _vp, _sz, _i, _vp]),
     "kvp_probe_read_tiled": (_i, [_vp, _sz, _vp, _i, _i, _i, _i, _vp]),
@@ -106,6 +108,18 @@ def check(status: int) -> None:
     if status != KVP_OK:
         cls = _ERRORS.get(status, KvpError)
         raise cls(last_error() or f"libkvpack status {status}")
+
+
+def set_tuning(key: str, value: int) -> None:
+    """Override one kernel-selection choice (-1 restores the library's);
+    see include/kvpack.h kvp_set_tuning."""
+    check(load().kvp_set_tuning(key.encode(), int(value)))
+
+
+def get_tuning(key: str) -> int:
+    v = ctypes.c_int()
+    check(load().kvp_get_tuning(key.encode(), ctypes.byref(v)))
+    return v.value
 
 
 def version() -> str:

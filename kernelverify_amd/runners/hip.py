@@ -14,6 +14,16 @@ Each timed repeat is bracketed by HIP events on the runner's own stream
 (`gpu_seconds`) and by the host clock from launch to completion
 (`wall_seconds`). Outputs are copied back after the last repeat.
 
+`case_timeout` is a host-clock deadline per case, checked while the case's
+work is still on the device: the runner polls its stop event
+(hipEventQuery) instead of blocking on it, so a kernel that never finishes
+is reported as TIMEOUT. Its queue is then still busy, so the runner is
+`wedged`: every later case gets TIMEOUT without touching the device, and
+the timed-out case's buffers are kept alive (never freed under a kernel
+that may still write them). The process cannot reclaim that queue; the
+gate drivers exit non-zero when any case timed out, and a caller should
+end the process. It is not re-executed in place.
+
 Candidates run in this process, one at a time, on one stream: the kernels
 under test are the pack library's and kernels compiled from source here.
 The runner does not sandbox a candidate; one that writes outside its
@@ -73,6 +83,9 @@ class HipRunner:
     warmup: int = DEFAULT_WARMUP
     repeats: int = DEFAULT_REPEATS
     device: int = 0
+    # set once a case overran case_timeout with its work still queued
+    wedged: str = ""
+    _abandoned: list = field(default_factory=list, repr=False)
 
     # -- device ------------------------------------------------------------
     def probe(self) -> DeviceInfo | None:
@@ -146,9 +159,15 @@ class HipRunner:
                         for c in cases]
         results = []
         for case in cases:
+            if self.wedged:
+                results.append(RunResult(RunStatus.TIMEOUT, label=case.label,
+                                         detail=f"not run: {self.wedged}"))
+                continue
             results.append(self._run_case(spec, module, case, warmup, repeats, stream))
-        if module is not None:
+        if module is not None and not self.wedged:
             module.unload()
+        elif module is not None:
+            self._abandoned.append(module)
         return results
 
     def _run_case(self, spec, module, case: RunCase, warmup: int, repeats: int,
@@ -173,14 +192,24 @@ class HipRunner:
             return RunResult(st, detail=detail, label=case.label)
 
         handle = stream.handle
-        start_all = time.perf_counter()
+        deadline = time.perf_counter() + self.case_timeout
+        start, stop = hip.Event(), hip.Event()
+
+        def overran() -> RunResult:
+            self.wedged = (f"case {case.label!r} ran past case_timeout = {self.case_timeout:g} s "
+                           "and its work is still queued on the device")
+            self._abandoned.append(bound)
+            return RunResult(RunStatus.TIMEOUT, label=case.label,
+                             detail=f"still running after {self.case_timeout:g} s")
+
         for _ in range(warmup):
             code = bound.launch(handle)
             if code:
                 return failure(code)
-        stream.synchronize()
+        stop.record(stream)
+        if not stop.wait_until(deadline):
+            return overran()
         gpu, wall = [], []
-        start, stop = hip.Event(), hip.Event()
         for _ in range(max(repeats, 1)):
             t0 = time.perf_counter()
             start.record(stream)
@@ -188,12 +217,10 @@ class HipRunner:
             if code:
                 return failure(code)
             stop.record(stream)
-            stop.synchronize()
+            if not stop.wait_until(deadline):
+                return overran()
             wall.append(time.perf_counter() - t0)
             gpu.append(start.elapsed_ms(stop) * 1e-3)
-            if time.perf_counter() - start_all > self.case_timeout:
-                return RunResult(RunStatus.TIMEOUT, label=case.label,
-                                 detail=f"the case ran past {self.case_timeout:g} s")
         outputs = [o.to_host() for o in bound.outputs]
         return RunResult(RunStatus.OK, outputs=outputs, label=case.label,
                          timing=Timing(tuple(gpu), tuple(wall), warmup))

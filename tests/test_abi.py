@@ -65,3 +65,25 @@ def test_binding_arities_match_header():
     assert set(arities) == set(lib.SIGNATURES)
     for name, (_, args) in lib.SIGNATURES.items():
         assert len(args) == arities[name], (name, len(args), arities[name])
+
+
+def test_tuning_keys_are_explicit_and_restorable():
+    """Kernel selection changes only through kvp_set_tuning (no environment
+    variable is read); unknown keys are refused and -1 restores the
+    library's choice."""
+    assert lib.get_tuning("qmv_path") == -1
+    lib.set_tuning("qmv_path", 5)
+    try:
+        assert lib.get_tuning("qmv_path") == 5
+    finally:
+        lib.set_tuning("qmv_path", -1)
+    assert lib.get_tuning("qmv_path") == -1
+    with pytest.raises(lib.InvalidArgument):
+        lib.set_tuning("no_such_key", 1)
+    with pytest.raises(lib.InvalidArgument):
+        lib.set_tuning("moe_kq", -2)
+
+    src = Path(__file__).resolve().parents[1] / "kernelverify_amd" / "csrc"
+    for f in src.iterdir():
+        if f.suffix in (".hip", ".h"):
+            assert "getenv" not in f.read_text(), f.name

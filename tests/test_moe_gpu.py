@@ -17,6 +17,7 @@ Outputs: the oracle's fp64 reference and ensemble-floor tolerance.
 import numpy as np
 import pytest
 
+from kernelverify_amd import lib
 from kernelverify_amd.pack import moe_dispatch as moe
 from kernelverify_amd.pack.codes import pack_codes
 from oracle.extensions import (
@@ -136,6 +137,31 @@ def test_reference_gate_k2(shape, mode):
     idx, gate = moe.route(x=x, router=router, k=2)
     out = moe.dispatch_host(x, idx, gate, packed, scales, biases, bits=4)
     v = verify_output("moe_dispatch", moe_inputs(x, router, arts), out)
+    assert v.ok, v
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_dispatch_slot_naming_no_expert_adds_nothing(bits):
+    """A slot whose index is n_experts or more contributes zero (as in
+    kvp_moe_swiglu): the output equals the reference with that slot's gate
+    zeroed, and a token with no valid slot is zero."""
+    rng = np.random.default_rng(90 + bits)
+    n, d, e, k, d_out = 4, 256, 8, 3, 96
+    x = rng.standard_normal((n, d)).astype(np.float16)
+    experts = (rng.standard_normal((e, d_out, d)) * 0.02).astype(np.float16)
+    packed, scales, biases, arts = quantize_experts(experts, bits)
+    idx, gate = route_topk(rng.standard_normal((n, e)).astype(np.float32), k)
+    idx = idx.astype(np.uint32)
+    bad = idx.copy()
+    bad[1, 2] = e
+    bad[3, :] = np.uint32(0xFFFFFFFF)
+    out = moe.dispatch_host(x, bad, gate, packed, scales, biases, bits=bits, out_dtype="float32")
+    assert not np.any(out[3])
+    fixed, g0 = idx.copy(), gate.copy()
+    fixed[1, 2], g0[1, 2] = 0, 0.0
+    fixed[3, :], g0[3, :] = 0, 0.0
+    ref = moe_linear_reference(x, fixed, g0, arts)
+    v = judge(out, ref, moe_linear_tolerance("float32", x, fixed, g0, arts, ref))
     assert v.ok, v
 
 
@@ -269,10 +295,10 @@ def test_one_token_at_every_width(bits):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_in_block_routing_equals_the_permute_launch(bits, monkeypatch):
+def test_in_block_routing_equals_the_permute_launch(bits):
     """A few pairs on the matrix cores: the gate/up launch builds the
     permutation in-block. Its output is bit-identical to the separate
-    permute launch (KVP_MOE_PERMUTE=1), also when one pair names no expert
+    permute launch (tuning key moe_permute = 1), also when one pair names no expert
     (that pair adds nothing: the reference with its gate zeroed) and when
     none does (zeros)."""
     x, mats, logits = swiglu_case(6, 16, 512, 256, bits, seed=70 + bits)
@@ -282,14 +308,16 @@ def test_in_block_routing_equals_the_permute_launch(bits, monkeypatch):
     bad[2, 1] = 16
     none = np.full_like(idx, 99)
     outs = {}
-    for name, ids in (("routed", idx), ("one-invalid", bad), ("none-valid", none)):
-        monkeypatch.delenv("KVP_MOE_PERMUTE", raising=False)
-        fused = run_swiglu(x, mats, ids, gate, bits, "float32")
-        monkeypatch.setenv("KVP_MOE_PERMUTE", "1")
-        separate = run_swiglu(x, mats, ids, gate, bits, "float32")
-        assert np.array_equal(fused, separate), name
-        outs[name] = fused
-    monkeypatch.delenv("KVP_MOE_PERMUTE", raising=False)
+    try:
+        for name, ids in (("routed", idx), ("one-invalid", bad), ("none-valid", none)):
+            lib.set_tuning("moe_permute", -1)
+            fused = run_swiglu(x, mats, ids, gate, bits, "float32")
+            lib.set_tuning("moe_permute", 1)
+            separate = run_swiglu(x, mats, ids, gate, bits, "float32")
+            assert np.array_equal(fused, separate), name
+            outs[name] = fused
+    finally:
+        lib.set_tuning("moe_permute", -1)
     assert not np.any(outs["none-valid"])
     v = judge_swiglu(x, mats, idx, gate, outs["routed"], None, "float32")
     assert v.ok, v
@@ -300,18 +328,19 @@ def test_in_block_routing_equals_the_permute_launch(bits, monkeypatch):
 
 
 @pytest.mark.parametrize("n", [64, 65])
-def test_in_block_routing_limit(n, monkeypatch):
+def test_in_block_routing_limit(n):
     """n * k = 512 pairs is the largest in-block routing (bit-identical to
     the permute launch); 520 takes the permute launch. Both against the
     oracle on three tokens."""
     x, mats, logits = swiglu_case(n, 128, 512, 256, 4, seed=80 + n)
     idx, gate = route_topk(logits, 8)
     idx = idx.astype(np.uint32)
-    monkeypatch.delenv("KVP_MOE_PERMUTE", raising=False)
     out = run_swiglu(x, mats, idx, gate, 4, "float32")
     if n * 8 <= 512:
-        monkeypatch.setenv("KVP_MOE_PERMUTE", "1")
-        assert np.array_equal(out, run_swiglu(x, mats, idx, gate, 4, "float32"))
-        monkeypatch.delenv("KVP_MOE_PERMUTE")
+        lib.set_tuning("moe_permute", 1)
+        try:
+            assert np.array_equal(out, run_swiglu(x, mats, idx, gate, 4, "float32"))
+        finally:
+            lib.set_tuning("moe_permute", -1)
     v = judge_swiglu(x, mats, idx, gate, out, [0, n // 2, n - 1], "float32")
     assert v.ok, v

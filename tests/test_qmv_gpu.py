@@ -141,3 +141,23 @@ def test_single_pass_is_linear_in_x():
     lhs = parts[:2] + parts[2:]
     scale = np.abs(whole).max()
     assert np.max(np.abs(lhs - whole)) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("d_out,d_in", [(4099, 2560), (1001, 4096), (70001, 256)])
+def test_persistent_m1_kernel_every_width(bits, d_out, d_in):
+    """The persistent M = 1 kernel (waves walking row sets through a ring),
+    forced with tuning key qmv_path = 5 on shapes whose d_out is not a
+    multiple of its two-row set and, for 70001 rows, of the grid's waves;
+    judged on all rows against the oracle."""
+    from kernelverify_amd import lib
+
+    x, q, s, b = draw_qmv(d_out, d_in, bits, 1, seed=bits * 7 + d_out)
+    art = artefact_from_arrays(q, s, b, bits)
+    lib.set_tuning("qmv_path", 5)
+    try:
+        got = run_gpu(x, art, bits, "float32")
+    finally:
+        lib.set_tuning("qmv_path", -1)
+    v = gate(x, art, got, "float32")
+    assert v.ok, (bits, d_out, d_in, v)

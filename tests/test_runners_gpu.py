@@ -99,3 +99,40 @@ def test_interleaved_compare_reports_rounds():
     assert not report.failure, report.failure
     assert len(report.cases[0].samples) == 3
     assert np.isfinite(report.cases[0].speedup)
+
+
+# A kernel that waits a bounded time on the device's constant 100 MHz wall
+# clock, then writes its output: it always finishes (at most `ticks` ticks
+# and at most 2^26 polls), but longer than the runner's deadline below.
+WAIT = """
+extern "C" __global__ void wait_then_write(float* y, unsigned ticks) {
+  const unsigned long long t0 = wall_clock64();
+  unsigned polls = 0;
+  while (wall_clock64() - t0 < ticks && polls < (1u << 26)) ++polls;
+  y[threadIdx.x] = 1.0f + (float)min(polls, 1u);  // 1 or 2: the kernel ran
+}
+"""
+
+
+def test_a_case_still_running_at_its_deadline_is_timeout_and_wedges_the_runner():
+    """case_timeout is a host deadline checked while the work is queued: a
+    case whose kernel outlives it is TIMEOUT, and the runner refuses the
+    rest of its cases without touching the device."""
+    spec = KernelSpec(source=WAIT, entry_point="wait_then_write",
+                      bindings=(Binding(BindingKind.OUTPUT),
+                                Binding(BindingKind.SCALAR, "ticks", "uint32")),
+                      launch=LaunchSpec(grid=(64, 1, 1), threadgroup=(64, 1, 1)))
+    slow = RunCase(inputs={}, params={"ticks": 20_000_000}, output_shapes=[((64,), "float32")],
+                   label="200 ms")
+    quick = RunCase(inputs={}, params={"ticks": 1}, output_shapes=[((64,), "float32")],
+                    label="quick")
+    ok = HipRunner(warmup=0, repeats=1).run(spec, [quick])
+    assert ok[0].ok and np.all(ok[0].outputs[0] >= 1.0)
+    runner = HipRunner(case_timeout=0.02, warmup=0, repeats=1)
+    res = runner.run(spec, [slow, quick])
+    assert res[0].status is RunStatus.TIMEOUT and "still running" in res[0].detail
+    assert res[1].status is RunStatus.TIMEOUT and res[1].detail.startswith("not run")
+    assert runner.wedged
+    from kernelverify_amd import hip
+
+    hip.synchronize()  # the slow kernel ends by itself (bounded above)
