@@ -135,19 +135,24 @@ __global__ __launch_bounds__(kBlock) void kv_combine_kernel(KvArgs a) {
   __shared__ float gm[kCombGroups], gl[kCombGroups];
   __shared__ float go[kCombGroups][kCombDims];
 
-  // Entries 0 .. nc - 1 are the chunks, entry nc the new token (slot n_chunks).
+  // Slots 0 .. nc - 1 are the chunks, slot n_chunks the new token. Every
+  // slot's loads go out with the length's (they need not wait for it); the
+  // slots from nc to n_chunks - 1 hold no partial of this call and are
+  // skipped, never used in arithmetic.
   const float* pz = a.part + (size_t)z * (a.n_chunks + 1) * partial_floats(DH);
   const int dd = threadIdx.x % kCombDims, grp = threadIdx.x / kCombDims;
   float M = -INFINITY, L = 0.0f, O = 0.0f;
 #pragma unroll 4
-  for (int c = grp; c <= nc; c += kCombGroups) {
-    const float* pc = pz + (c < nc ? c : a.n_chunks) * partial_floats(DH);
+  for (int c = grp; c <= a.n_chunks; c += kCombGroups) {
+    const float* pc = pz + c * partial_floats(DH);
     const float mc = pc[0], lc = pc[1], oc = pc[2 + d0 + dd];
-    const float mn = fmaxf(M, mc);
-    const float ea = exp2f(M - mn), eb = exp2f(mc - mn);  // first entry: ea = 2^-inf = 0
-    L = fmaf(L, ea, lc * eb);
-    O = fmaf(O, ea, oc * eb);
-    M = mn;
+    if (c < nc || c == a.n_chunks) {
+      const float mn = fmaxf(M, mc);
+      const float ea = exp2f(M - mn), eb = exp2f(mc - mn);  // first entry: ea = 2^-inf = 0
+      L = fmaf(L, ea, lc * eb);
+      O = fmaf(O, ea, oc * eb);
+      M = mn;
+    }
   }
   go[grp][dd] = O;
   if (dd == 0) {
@@ -619,40 +624,40 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   __shared__ float qss_sh[G][kGroups];
   __shared__ __align__(16) float xbuf[kWaves][kXWave];
   __shared__ float wm[kWaves][G], wl[kWaves][G];
-  __shared__ __align__(16) float wo[kWaves][G][DH];
+  __shared__ __align__(16) float wo[kWaves][G][DH];   // hi parts, + p * b
+  __shared__ __align__(16) float wol[kWaves][G][DH];  // lo parts
 
   const int c = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  const int T = min(max(a.t_cached[b], 0), a.t_stride);
   const int slice0 = c * a.chunk;
-  if (slice0 >= T) {  // block-uniform
-    if (c == 0) write_new_entry<DH, G>(a, b, hk);
-    return;
-  }
-  const int n = min(a.chunk, T - slice0);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int n16 = lane % 16, q4 = lane / 16;
   const int h0 = hk * G;
   const size_t base = ((size_t)(a.per_seq ? b : 0) * a.n_kv_heads + hk) * a.t_stride + slice0;
-  const int nsteps = (n + kP - 1) / kP;
   float* xw = xbuf[wave];
   auto xaddr = [](int pos, int g, int h) { return pos * kXS + (pos / 8) * 8 + g * kHp + h; };
 
+  // The slice's cache loads do not wait for the length: they cover the
+  // slice within t_stride (every block of the grid starts inside it), the
+  // length load travels beside them, and positions at or past T are masked
+  // out of the softmax (their scores are -inf, so p = 0 and they add
+  // nothing). Only a block wholly past its sequence's end wastes its first
+  // step's loads.
+  const int n_max = min(a.chunk, a.t_stride - slice0);
   SliceRsrc rs;
   {
     const uint32_t rb = S::kRowWords * 4, sb = 2 * kGroups;
-    rs.kw = slice_rsrc(a.k_wq + base * S::kRowWords, n * rb);
-    rs.vw = slice_rsrc(a.v_wq + base * S::kRowWords, n * rb);
-    rs.ks = slice_rsrc(a.k_s + base * kGroups, n * sb);
-    rs.kb = slice_rsrc(a.k_b + base * kGroups, n * sb);
-    rs.vs = slice_rsrc(a.v_s + base * kGroups, n * sb);
-    rs.vb = slice_rsrc(a.v_b + base * kGroups, n * sb);
+    rs.kw = slice_rsrc(a.k_wq + base * S::kRowWords, n_max * rb);
+    rs.vw = slice_rsrc(a.v_wq + base * S::kRowWords, n_max * rb);
+    rs.ks = slice_rsrc(a.k_s + base * kGroups, n_max * sb);
+    rs.kb = slice_rsrc(a.k_b + base * kGroups, n_max * sb);
+    rs.vs = slice_rsrc(a.v_s + base * kGroups, n_max * sb);
+    rs.vb = slice_rsrc(a.v_b + base * kGroups, n_max * sb);
   }
   // Double-buffered: the next step's loads are in flight while this one is
   // processed. A step past the last one loads from one past the slice: out
   // of the buffers' range, it reads zeros without traffic.
   KvStepRegs<BITS, DH, G> RA, RB;
-  auto step_pos = [&](int t) { return t < nsteps ? kP * t : a.chunk + kP; };
   // The small inputs go out before the first cache loads, so (returns being
   // in order) they are in registers while the cache is still in flight: the
   // query table (G rows, then a zero row; at most one 16-byte item per
@@ -680,7 +685,16 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
       }
     }
   }
-  if (wave < nsteps) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
+
+  if (wave * kP < n_max) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
+  const int T = min(max(a.t_cached[b], 0), a.t_stride);
+  if (slice0 >= T) {  // block-uniform
+    if (c == 0) write_new_entry<DH, G>(a, b, hk);
+    return;
+  }
+  const int n = min(a.chunk, T - slice0);
+  const int nsteps = (n + kP - 1) / kP;
+  auto step_pos = [&](int t) { return t < nsteps ? kP * t : a.chunk + kP; };
 
   if (qi_row <= G) *reinterpret_cast<u32x4*>(&qtab[qi_row * DH + 8 * qi_c8]) = qv;
   // The new entry's partial (slot n_chunks: m = q . new_k * scale, l = 1,
@@ -785,10 +799,16 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
         sv[i] = v;
       }
     }
+    // V scale and bias of this lane's score position; positions past the
+    // sequence's end (read only in its partial last step) get zeros, so
+    // whatever a padded cache holds there (even NaN patterns) adds nothing.
+    uint32_t vs_l = R.vs, vb_l = R.vbias;
     if (p0 + kP > n) {  // the slice's partial last step (uniform)
       const bool valid = p0 + spos < n;
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[i] = valid ? sv[i] : -INFINITY;
+      vs_l = valid ? vs_l : 0u;
+      vb_l = valid ? vb_l : 0u;
     }
     // --- the max in use: moves only when a score outruns it by 2^kLazy ---------
     uint64_t rise = 0;
@@ -798,7 +818,7 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
         rise |= __builtin_amdgcn_ballot_w64(sv[i] > mrow[i] + kLazy);
     const bool raise = rise != 0;  // wave-uniform
     // --- range shift: a V scale larger than the current E admits -----------------
-    const uint32_t ub = R.vs & 0x7FFF7FFFu;
+    const uint32_t ub = vs_l & 0x7FFF7FFFu;
     const bool over = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
                                                        __builtin_bit_cast(u16x2, ub),
                                                        __builtin_bit_cast(u16x2, thr))) != thr;
@@ -865,8 +885,8 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     const float sE0 = exp2_int(E0), sE1 = exp2_int(E1);
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) {
-      const float vsg = f16_bits_to_f32((uint16_t)(R.vs >> (16 * g))) * (g ? sE1 : sE0);
-      const float vbg = f16_bits_to_f32((uint16_t)(R.vbias >> (16 * g)));
+      const float vsg = f16_bits_to_f32((uint16_t)(vs_l >> (16 * g))) * (g ? sE1 : sE0);
+      const float vbg = f16_bits_to_f32((uint16_t)(vb_l >> (16 * g)));
       f32x4 x;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -970,32 +990,29 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     }
   }
   const float inv0 = exp2_int(24 - E0), inv1 = exp2_int(24 - E1);
-  // hi + lo: the lo rows sit one 16-lane row up (DH 128) or 32 lanes up
-  // (DH 64). (A plain lane exchange: the two-result lane-swap builtins gave
-  // inconsistent result orders in this compiler.)
-  auto add_lo = [](float v) { return v + __shfl_xor(v, DH == 128 ? 16 : 32, kWave); };
+  // The hi and lo parts of x land in different D rows (the lo rows one
+  // 16-lane row up at DH 128, 32 lanes up at DH 64): each part goes to LDS
+  // as it is (wo, wol) and the merge below adds them, with no lane exchange.
+  const bool is_lo = DH == 128 ? (q4 & 1) != 0 : q4 >= 2;
 #pragma unroll
   for (int st = 0; st < kSets; ++st)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float o[S::kNB];
-#pragma unroll
-      for (int nb = 0; nb < S::kNB; ++nb) o[nb] = add_lo(acc[st][nb][i]);
       int h, d0;
       bool keep;
       float ig, pbv;
       if constexpr (DH == 128) {
-        // lanes of rows 0 (group 0, dims 0-63) and 2 (group 1, dims 64-127)
+        // rows 0/1 (group 0, dims 0-63) and 2/3 (group 1, dims 64-127)
         const int g = q4 >> 1;
         h = 4 * st + i;
-        keep = (q4 & 1) == 0 && (n16 >> 3) == g && h < G;
+        keep = (n16 >> 3) == g && h < G;
         const int hc = min(i, (st == 0 ? G : G - 4) - 1);
         ig = g ? inv1 : inv0;
         pbv = st == 0 ? (g ? pA1[hc] : pA0[hc]) : (g ? pB1[hc] : pB0[hc]);
         d0 = 8 * n16;
       } else {
-        h = 4 * q4 + i;
-        keep = q4 < 2 && h < G;
+        h = 4 * (q4 & 1) + i;
+        keep = h < G;
         ig = inv0;
         if constexpr (G > 4)
           pbv = (q4 & 1) ? pB0[i] : pA0[i];
@@ -1003,12 +1020,17 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
           pbv = pA0[min(i, G - 1)];
         d0 = value_dim<BITS, DH>(n16, 0);
       }
+      pbv = is_lo ? 0.0f : pbv;  // p * b enters once, with the hi part
+      float* dst = is_lo ? &wol[wave][h][d0] : &wo[wave][h][d0];
       if (keep) {
 #pragma unroll
-        for (int v4 = 0; v4 < S::kNB / 4; ++v4)
-          *reinterpret_cast<f32x4*>(&wo[wave][h][d0 + 4 * v4]) =
-              f32x4{fmaf(o[4 * v4], ig, pbv), fmaf(o[4 * v4 + 1], ig, pbv),
-                    fmaf(o[4 * v4 + 2], ig, pbv), fmaf(o[4 * v4 + 3], ig, pbv)};
+        for (int v4 = 0; v4 < S::kNB / 4; ++v4) {
+          const f32x4 o = {acc[st][4 * v4][i], acc[st][4 * v4 + 1][i], acc[st][4 * v4 + 2][i],
+                           acc[st][4 * v4 + 3][i]};
+          *reinterpret_cast<f32x4*>(dst + 4 * v4) =
+              f32x4{fmaf(o[0], ig, pbv), fmaf(o[1], ig, pbv), fmaf(o[2], ig, pbv),
+                    fmaf(o[3], ig, pbv)};
+        }
       }
     }
   if (lane == 0) {
@@ -1030,7 +1052,7 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     for (int w = 0; w < kWaves; ++w) {
       const float e = wl[w][g] > 0.0f ? exp2f(wm[w][g] - M) : 0.0f;  // idle waves hold -inf
       L = fmaf(wl[w][g], e, L);
-      O = fmaf(wo[w][g][dd], e, O);
+      O = fmaf(wo[w][g][dd] + wol[w][g][dd], e, O);
     }
     float* pp = a.part + (((size_t)b * a.n_heads + h0 + g) * (a.n_chunks + 1) + c) * partial_floats(DH);
     pp[2 + dd] = O;

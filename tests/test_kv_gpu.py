@@ -303,3 +303,40 @@ def test_all_zero_values():
     out = run(q, kc, vc, nk, nv, 4, "float32")
     v = verify_output("kv_attention", kv_gqa_inputs(q, kc, vc, nk, nv, 4), out, dtype="float32")
     assert v.ok, v
+
+
+def test_one_workspace_serves_calls_of_every_shape():
+    """One workspace serves calls of different shapes in turn (an empty
+    sequence among them): nothing one call leaves in it changes the next,
+    and each output passes the oracle."""
+    from kernelverify_amd import hip
+    from kernelverify_amd.hip import DeviceArray
+
+    ws = DeviceArray((8 << 20,), np.uint8)
+    ws.fill_byte(0x7F)
+    cases = [(1, 32, 8, 5000, 4, [5000]), (3, 8, 2, 2600, 8, [100, 0, 2600]),
+             (2, 16, 2, 3000, 4, [3000, 1])]
+    for b, h, hkv, t_stride, bits, lengths in cases:
+        rng = np.random.default_rng(b * 100 + h)
+        q = (rng.standard_normal((b, h, 128)) * 0.3).astype(np.float16)
+        kc = rng.standard_normal((b, hkv, t_stride, 128)).astype(np.float16)
+        vc = rng.standard_normal((b, hkv, t_stride, 128)).astype(np.float16)
+        nk = (rng.standard_normal((b, hkv, 128)) * 0.3).astype(np.float16)
+        nv = rng.standard_normal((b, hkv, 128)).astype(np.float16)
+        dev = [DeviceArray.from_host(np.ascontiguousarray(a)) for a in
+               (q, *quantize_cache(kc, bits), *quantize_cache(vc, bits), nk, nv)]
+        t_dev = DeviceArray.from_host(np.array(lengths, dtype=np.int32))
+        out = DeviceArray((b, h, 128), "float32")
+        kv_attention.KvDecodeCall(*dev, t_dev, out, bits=bits, cache_per_sequence=True,
+                                  workspace=ws)()
+        hip.synchronize()
+        got = out.to_host()
+        for i, t in enumerate(lengths):
+            if t == 0:  # the softmax has one term: out = new_v of the head's KV head
+                want = np.repeat(nv[i].astype(np.float32), h // hkv, axis=0)
+                assert np.max(np.abs(got[i] - want)) <= 1e-6 * np.max(np.abs(want))
+                continue
+            ref, tols = kv_per_sequence(q[i:i + 1], kc[i:i + 1], vc[i:i + 1], nk[i:i + 1],
+                                        nv[i:i + 1], [t], bits, dtype="float32")
+            v = judge(got[i:i + 1], ref, tols[0])
+            assert v.ok, (b, h, bits, i, v)
