@@ -206,7 +206,8 @@ class KvWorkload:
 class MoeWorkload:
     """One MoE decode step of BASELINE config 5: route top-8 of 128 experts
     from fp32 N(0, 1) logits, then the SwiGLU experts (gate/up 768 x 2048,
-    down 2048 x 768, 4-bit) for n tokens. Expert sets rotate over >= 1 GiB."""
+    down 2048 x 768, 4-bit) for n tokens, as one kvp_moe_route_swiglu call.
+    Expert sets rotate over >= 1 GiB."""
 
     def __init__(self, n, n_experts=128, k=8, d_model=2048, d_ffn=768, bits=4, seed=0):
         from kernelverify_amd import hip
@@ -232,14 +233,13 @@ class MoeWorkload:
         self.idx = DeviceArray((n, k), np.uint32)
         self.gate = DeviceArray((n, k), np.float32)
         self.out = DeviceArray((n, d_model), np.float16)
-        self._route = moe.route_logits
         self.calls = []
         ws = None
         for i in range(copies):
             m = mats if i == 0 else [tuple(DeviceArray.from_host(a.to_host()) for a in t)
                                      for t in mats]
             call = moe.SwigluCall(self.dx, self.idx, self.gate, *m, self.out, bits=bits,
-                                  workspace=ws)
+                                  workspace=ws, logits=self.dl)
             ws = call.workspace
             self.calls.append(call)
         moe.route_logits(self.dl, self.idx, self.gate, k)
@@ -250,7 +250,7 @@ class MoeWorkload:
         self.i = 0
 
     def step(self, stream):
-        self._route(self.dl, self.idx, self.gate, self.k, stream)
+        # routing from the logits and the experts: one kvp_moe_route_swiglu
         self.calls[self.i % len(self.calls)](stream)
         self.i += 1
 

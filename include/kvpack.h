@@ -220,6 +220,22 @@ int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* gate,
 int kvp_set_tuning(const char* key, int value);
 int kvp_get_tuning(const char* key, int* value);
 
+/* Routing from logits and the SwiGLU experts in one call: the result of
+ * kvp_moe_route_logits (idx, gate written as it writes them) followed by
+ * kvp_moe_swiglu, same arguments and workspace. For up to 4 tokens on the
+ * 4/8-bit matrix-core path (n * k <= 512, n_experts <= 256) every gate/up
+ * block routes the tokens itself, so no routing launch precedes the experts;
+ * otherwise the routing kernel runs first. No reference counterpart: the
+ * reference's routing and dispatch are separate kernels
+ * (kernelverify/pack/moe_dispatch.py:39-138). */
+int kvp_moe_route_swiglu(const float* logits, const void* x, uint32_t* idx, float* gate,
+                         const uint32_t* gate_wq, const void* gate_scales,
+                         const void* gate_biases, const uint32_t* up_wq, const void* up_scales,
+                         const void* up_biases, const uint32_t* down_wq, const void* down_scales,
+                         const void* down_biases, void* out, int out_dtype, int n, int k,
+                         int n_experts, int d_model, int d_ffn, int bits, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* HBM roofline probe kernels (replaces bench/metal/roofline_probe.mm:35-144
  * stream_read / stream_copy). `n_bytes` multiple of 16. read_sink receives a
  * per-block value so the loads cannot be removed. */

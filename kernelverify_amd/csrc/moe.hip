@@ -72,7 +72,8 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 // logits: E fp32 values of one token, held as E/64 per lane (lane-strided).
 template <int EPL>
 __device__ __forceinline__ void route_token(const float (&lg)[EPL], int n_experts, int k,
-                                            uint32_t* __restrict__ idx, float* __restrict__ gate) {
+                                            uint32_t* __restrict__ idx, float* __restrict__ gate,
+                                            uint32_t* idx2 = nullptr, float* gate2 = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   float peak = -INFINITY;
 #pragma unroll
@@ -118,6 +119,10 @@ __device__ __forceinline__ void route_token(const float (&lg)[EPL], int n_expert
     for (int s = 0; s < k; ++s) {
       idx[s] = (uint32_t)chosen_i[s];
       gate[s] = chosen_p[s] / total;
+      if (idx2) {
+        idx2[s] = (uint32_t)chosen_i[s];
+        gate2[s] = chosen_p[s] / total;
+      }
     }
   }
 }
@@ -269,6 +274,13 @@ struct ExpertArgs {
   // indices in, and the permute kernel's tables out for the launches after.
   const uint32_t* idx;     // [pairs]
   int pairs, n_experts;
+  // In-block routing from logits (kvp_moe_route_swiglu, a few tokens): the
+  // launch routes every token itself (the logits-door contract) instead of
+  // reading idx; block (0, 0) also writes the routing to out_idx / out_gate.
+  const float* logits;     // [n][n_experts] fp32, or null
+  int n_tokens, epl;       // tokens; experts per lane (1, 2 or 4)
+  uint32_t* out_idx;       // [n][k]
+  float* out_gate;         // [n][k]
   int32_t* t_offsets;      // [E+1]: entries e and e + 1 of every routed e
   int32_t* t_perm;         // [pairs]
   int32_t* t_active;       // [1 + E]
@@ -277,11 +289,35 @@ struct ExpertArgs {
 
 // Pairs (n * k) up to which the gate/up launch builds its routing in-block.
 constexpr int kFusedPairs = 512;
+// Tokens up to which kvp_moe_route_swiglu routes inside the gate/up launch
+// (each block routes every token, one per wave: measured, two per wave
+// cost the gate/up blocks more than the routing launch they replace).
+constexpr int kRouteTokensInBlock = 4;
 
 struct BlockRoute {
   int e, p0, p1;           // the expert and its segment [p0, p1) of the sorted order
   const int32_t* seg;      // LDS: the segment's flat pair indices, in flat order
 };
+
+// Every token's routing, computed by this block from the logits (wave w
+// routes tokens w, w + 4, ...), into the LDS tile; the launch's first block
+// also writes it to the routing outputs.
+template <int EPL>
+__device__ void route_tokens_in_block(const ExpertArgs& a, uint32_t* tile, float* gate_sh,
+                                      bool write_out) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  for (int t = wave; t < a.n_tokens; t += kWaves) {  // wave-uniform
+    float lg[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + j * kWave;
+      lg[j] = e < a.n_experts ? a.logits[(size_t)t * a.n_experts + e] : 0.0f;
+    }
+    route_token<EPL>(lg, a.n_experts, a.k, tile + t * a.k, gate_sh + t * a.k,
+                     write_out ? a.out_idx + (size_t)t * a.k : nullptr,
+                     write_out ? a.out_gate + (size_t)t * a.k : nullptr);
+  }
+}
 
 // The permute kernel's result for one expert, built by one block from the
 // flat indices: e is the act-th routed expert in ascending order, its pairs
@@ -300,9 +336,18 @@ __device__ bool block_route(const ExpertArgs& a, int act, BlockRoute& br) {
   __shared__ int s_e, s_total, s_p0, s_n;
   const int pairs = a.pairs, n_experts = a.n_experts;
   for (int w = threadIdx.x; w < kMaxExperts / 32; w += kBlock) routed[w] = 0u;
+  if (a.logits) {  // route here: wave w takes tokens w, w + 4, ...
+    __shared__ float gate_sh[kFusedPairs];
+    const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+    switch (a.epl) {
+      case 1: route_tokens_in_block<1>(a, tile, gate_sh, first); break;
+      case 2: route_tokens_in_block<2>(a, tile, gate_sh, first); break;
+      default: route_tokens_in_block<4>(a, tile, gate_sh, first); break;
+    }
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < pairs; i += kBlock) {
-    const uint32_t e = a.idx[i];
+    const uint32_t e = a.logits ? tile[i] : a.idx[i];
     tile[i] = e;
     if (e < (uint32_t)n_experts) atomicOr(&routed[e >> 5], 1u << (e & 31));
   }
@@ -1129,29 +1174,32 @@ extern "C" int kvp_moe_dispatch(const void* x, const uint32_t* idx, const float*
   return set_error(KVP_UNSUPPORTED, "kvp_moe_dispatch: bits=%d", bits);
 }
 
-extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* gate,
-                              const uint32_t* gate_wq, const void* gate_scales,
-                              const void* gate_biases, const uint32_t* up_wq,
-                              const void* up_scales, const void* up_biases,
-                              const uint32_t* down_wq, const void* down_scales,
-                              const void* down_biases, void* out, int out_dtype, int n, int k,
-                              int n_experts, int d_model, int d_ffn, int bits, void* workspace,
-                              size_t workspace_bytes, void* stream) {
-  clear_error();
+namespace kvp {
+namespace {
+
+// kvp_moe_swiglu and kvp_moe_route_swiglu. With `logits` the routing is
+// computed here (into idx / gate): in the gate/up launch itself for a few
+// tokens on the in-block path, else by the routing kernel first.
+int swiglu_impl(const char* who, const float* logits, const void* x, uint32_t* idx, float* gate,
+                const uint32_t* gate_wq, const void* gate_scales, const void* gate_biases,
+                const uint32_t* up_wq, const void* up_scales, const void* up_biases,
+                const uint32_t* down_wq, const void* down_scales, const void* down_biases,
+                void* out, int out_dtype, int n, int k, int n_experts, int d_model, int d_ffn,
+                int bits, void* workspace, size_t workspace_bytes, void* stream) {
   KVP_REQUIRE(x && idx && gate && gate_wq && gate_scales && gate_biases && up_wq && up_scales &&
                   up_biases && down_wq && down_scales && down_biases && out,
-              "kvp_moe_swiglu: null pointer argument");
+              "%s: null pointer argument", who);
   KVP_REQUIRE(n >= 1 && k >= 1 && k <= kMaxK && n_experts >= 1 && n_experts <= kMaxExperts,
-              "kvp_moe_swiglu: n=%d k=%d n_experts=%d", n, k, n_experts);
-  KVP_REQUIRE((long long)n * k <= kPermuteTile, "kvp_moe_swiglu: n*k=%lld above %d",
+              "%s: n=%d k=%d n_experts=%d", who, n, k, n_experts);
+  KVP_REQUIRE((long long)n * k <= kPermuteTile, "%s: n*k=%lld above %d", who,
               (long long)n * k, kPermuteTile);
-  KVP_REQUIRE(out_dtype == KVP_F16 || out_dtype == KVP_F32, "kvp_moe_swiglu: out_dtype=%d",
+  KVP_REQUIRE(out_dtype == KVP_F16 || out_dtype == KVP_F32, "%s: out_dtype=%d", who,
               out_dtype);
   if (int rc = check_expert_dims("kvp_moe_swiglu (gate/up)", d_model, d_ffn, bits)) return rc;
   if (int rc = check_expert_dims("kvp_moe_swiglu (down)", d_ffn, d_model, bits)) return rc;
   const MoeLayout L = layout(n, k, n_experts, d_model, d_ffn);
   KVP_REQUIRE(workspace && workspace_bytes >= L.total,
-              "kvp_moe_swiglu: workspace of %zu bytes, %zu needed", workspace_bytes, L.total);
+              "%s: workspace of %zu bytes, %zu needed", who, workspace_bytes, L.total);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   int32_t* offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
@@ -1165,6 +1213,16 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
   // permutation in-block (tuning key moe_permute = 1 forces the permute launch).
   const bool route_in_block = pairs <= kFusedPairs && mfma_experts(bits, d_model) &&
                               tuning(kTuneMoePermute, 0) == 0;
+  // From logits, up to kRouteTokensInBlock tokens routed by every gate/up
+  // block (one per wave); more tokens take the routing kernel first.
+  const int epl = (n_experts + kWave - 1) / kWave;
+  const bool logits_in_block = logits && route_in_block && n <= kRouteTokensInBlock && epl <= 4;
+  if (logits) {
+    if (int rc = check_route_args(n, n_experts, k)) return rc;
+    if (!logits_in_block)
+      if (int rc = launch_route_core(logits, nullptr, nullptr, 0, idx, gate, n, n_experts, k, st))
+        return rc;
+  }
   if (!route_in_block) {
     hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(1024), 0, st, idx, offsets, perm, active,
                        slot_of, pairs, n_experts);
@@ -1189,6 +1247,13 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
   a.d_out = d_ffn;
   if (route_in_block) {
     a.idx = idx;
+    if (logits_in_block) {
+      a.logits = logits;
+      a.n_tokens = n;
+      a.epl = epl <= 1 ? 1 : (epl <= 2 ? 2 : 4);
+      a.out_idx = idx;
+      a.out_gate = gate;
+    }
     a.pairs = pairs;
     a.n_experts = n_experts;
     a.t_offsets = offsets;
@@ -1212,4 +1277,41 @@ extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* g
   dn.d_out = d_model;
   if (int rc = launch_experts_bits(bits, dn, max_active, false, true, st)) return rc;
   return launch_scatter(y, slot_of, gate, out, out_dtype, n, k, d_model, st);
+}
+
+}  // namespace
+}  // namespace kvp
+
+extern "C" int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* gate,
+                              const uint32_t* gate_wq, const void* gate_scales,
+                              const void* gate_biases, const uint32_t* up_wq,
+                              const void* up_scales, const void* up_biases,
+                              const uint32_t* down_wq, const void* down_scales,
+                              const void* down_biases, void* out, int out_dtype, int n, int k,
+                              int n_experts, int d_model, int d_ffn, int bits, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  using namespace kvp;
+  clear_error();
+  return swiglu_impl("kvp_moe_swiglu", nullptr, x, const_cast<uint32_t*>(idx),
+                     const_cast<float*>(gate), gate_wq, gate_scales, gate_biases, up_wq,
+                     up_scales, up_biases, down_wq, down_scales, down_biases, out, out_dtype, n,
+                     k, n_experts, d_model, d_ffn, bits, workspace, workspace_bytes, stream);
+}
+
+extern "C" int kvp_moe_route_swiglu(const float* logits, const void* x, uint32_t* idx,
+                                    float* gate, const uint32_t* gate_wq,
+                                    const void* gate_scales, const void* gate_biases,
+                                    const uint32_t* up_wq, const void* up_scales,
+                                    const void* up_biases, const uint32_t* down_wq,
+                                    const void* down_scales, const void* down_biases, void* out,
+                                    int out_dtype, int n, int k, int n_experts, int d_model,
+                                    int d_ffn, int bits, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  using namespace kvp;
+  clear_error();
+  KVP_REQUIRE(logits, "kvp_moe_route_swiglu: null logits");
+  return swiglu_impl("kvp_moe_route_swiglu", logits, x, idx, gate, gate_wq, gate_scales,
+                     gate_biases, up_wq, up_scales, up_biases, down_wq, down_scales, down_biases,
+                     out, out_dtype, n, k, n_experts, d_model, d_ffn, bits, workspace,
+                     workspace_bytes, stream);
 }

@@ -69,6 +69,7 @@ SIGNATURES = {
     "kvp_moe_dispatch": (_i, [_vp] * 7 + [_i] * 7 + [_vp]),
     "kvp_moe_swiglu_workspace_bytes": (_sz, [_i] * 5),
     "kvp_moe_swiglu": (_i, [_vp] * 13 + [_i] * 7 + [_vp, _sz, _vp]),
+    "kvp_moe_route_swiglu": (_i, [_vp] * 14 + [_i] * 7 + [_vp, _sz, _vp]),
     "kvp_set_tuning": (_i, [_cp, _i]),
     "kvp_get_tuning": (_i, [_cp, _ip]),
     "kvp_probe_stream_read": (_i, [_vp, _sz, _vp, _i, _vp]),

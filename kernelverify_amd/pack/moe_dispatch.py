@@ -110,10 +110,15 @@ def swiglu_workspace_bytes(n: int, k: int, n_experts: int, d_model: int, d_ffn: 
 
 
 class SwigluCall:
-    """One validated SwiGLU MoE step (bound arguments, own workspace)."""
+    """One validated SwiGLU MoE step (bound arguments, own workspace).
+
+    With ``logits`` (fp32 (n, E) on the device) the call routes too
+    (``kvp_moe_route_swiglu``): ``idx`` and ``gate`` are then outputs, written
+    as ``route_logits`` writes them."""
 
     def __init__(self, x: DeviceArray, idx: DeviceArray, gate: DeviceArray, gate_w, up_w,
-                 down_w, out: DeviceArray, *, bits: int, workspace: DeviceArray | None = None):
+                 down_w, out: DeviceArray, *, bits: int, workspace: DeviceArray | None = None,
+                 logits: DeviceArray | None = None):
         n, d_model = x.shape
         k = idx.shape[1]
         e, d_ffn, words = gate_w[0].shape
@@ -127,11 +132,18 @@ class SwigluCall:
         self.workspace = workspace if workspace is not None else DeviceArray((need,), np.uint8)
         if self.workspace.nbytes < need:
             raise lib.InvalidArgument(f"swiglu: workspace {self.workspace.nbytes} < {need}")
-        self._fn = lib.load().kvp_moe_swiglu
-        self._args = (x.ptr, idx.ptr, gate.ptr, *(a.ptr for a in (*gate_w, *up_w, *down_w)),
-                      out.ptr, OUT_DTYPES[out.dtype.name], n, k, e, d_model, d_ffn, bits,
-                      self.workspace.ptr, self.workspace.nbytes)
-        self._keep = (x, idx, gate, gate_w, up_w, down_w, out)
+        args = (x.ptr, idx.ptr, gate.ptr, *(a.ptr for a in (*gate_w, *up_w, *down_w)),
+                out.ptr, OUT_DTYPES[out.dtype.name], n, k, e, d_model, d_ffn, bits,
+                self.workspace.ptr, self.workspace.nbytes)
+        if logits is not None:
+            if logits.shape != (n, e) or logits.dtype != np.float32:
+                raise lib.InvalidArgument(f"swiglu: logits must be fp32 {(n, e)}")
+            self._fn = lib.load().kvp_moe_route_swiglu
+            self._args = (logits.ptr, *args)
+        else:
+            self._fn = lib.load().kvp_moe_swiglu
+            self._args = args
+        self._keep = (x, idx, gate, gate_w, up_w, down_w, out, logits)
 
     def __call__(self, stream=None) -> None:
         status = self._fn(*self._args, _h(stream))
@@ -188,6 +200,19 @@ def swiglu_host(x, idx, gate, gate_w, up_w, down_w, *, bits: int, out_dtype: str
     out = DeviceArray((x.shape[0], x.shape[1]), out_dtype)
     SwigluCall(dx, di, dg, up(gate_w), up(up_w), up(down_w), out, bits=bits)()
     return _sync_get(out)[0]
+
+
+def route_swiglu_host(x, logits, k, gate_w, up_w, down_w, *, bits: int,
+                      out_dtype: str = "float16"):
+    """Routing from logits and the experts in one call: (out, idx, gate)."""
+    up = lambda t: tuple(DeviceArray.from_host(np.ascontiguousarray(a)) for a in t)
+    n = x.shape[0]
+    dx = DeviceArray.from_host(np.ascontiguousarray(x, dtype=np.float16))
+    dl = DeviceArray.from_host(np.ascontiguousarray(logits, dtype=np.float32))
+    di, dg = DeviceArray((n, k), np.uint32), DeviceArray((n, k), np.float32)
+    out = DeviceArray((n, x.shape[1]), out_dtype)
+    SwigluCall(dx, di, dg, up(gate_w), up(up_w), up(down_w), out, bits=bits, logits=dl)()
+    return _sync_get(out, di, dg)
 
 
 # ---------------------------------------------------------------------------

@@ -344,3 +344,43 @@ def test_in_block_routing_limit(n):
             lib.set_tuning("moe_permute", -1)
     v = judge_swiglu(x, mats, idx, gate, out, [0, n // 2, n - 1], "float32")
     assert v.ok, v
+
+
+@pytest.mark.parametrize("n,e,k,bits", [(1, 128, 8, 4), (3, 64, 4, 8), (8, 128, 8, 4),
+                                        (12, 128, 8, 4), (2, 200, 6, 4), (4, 32, 4, 2)])
+def test_route_swiglu_equals_route_then_swiglu(n, e, k, bits):
+    """kvp_moe_route_swiglu (routing inside the gate/up launch for up to 4
+    tokens on the matrix cores, the routing kernel first otherwise) writes
+    the same indices and gates as kvp_moe_route_logits and the same output,
+    bit for bit, as kvp_moe_swiglu on that routing; the output also passes
+    the oracle on the contract's routing."""
+    d_model, d_ffn = 512, 256
+    x, mats, logits = swiglu_case(n, e, d_model, d_ffn, bits, seed=300 + n * e + bits)
+    assert not near_tie_rows(logits, k, ulps=64).any()
+    idx, gate = moe.route(logits, k)
+    want = run_swiglu(x, mats, idx, gate, bits, "float32")
+    got, idx2, gate2 = moe.route_swiglu_host(x, logits, k, mats["gate"][:3], mats["up"][:3],
+                                             mats["down"][:3], bits=bits, out_dtype="float32")
+    assert np.array_equal(idx2, idx) and np.array_equal(gate2, gate)
+    assert np.array_equal(got, want)
+    want_idx, want_gate = route_topk(logits, k)
+    assert np.array_equal(idx2.astype(np.int64), want_idx)
+    v = judge_swiglu(x, mats, want_idx, gate2, got, None, "float32")
+    assert v.ok, v
+
+
+def test_route_swiglu_config5_one_token_and_constant_logits():
+    """BASELINE config 5 at n = 1 through the fused call, and constant logits
+    (every expert ties: experts 0..k-1, gates 1/k)."""
+    x, mats, logits = swiglu_case(1, 128, 2048, 768, 4, seed=5)
+    out, idx, gate = moe.route_swiglu_host(x, logits, 8, mats["gate"][:3], mats["up"][:3],
+                                           mats["down"][:3], bits=4)
+    want_idx, _ = route_topk(logits, 8)
+    assert np.array_equal(idx.astype(np.int64), want_idx)
+    v = judge_swiglu(x, mats, want_idx, gate, out, None)
+    assert v.ok, v
+    flat = np.full((2, 128), 0.5, dtype=np.float32)
+    out, idx, gate = moe.route_swiglu_host(x[:1].repeat(2, 0), flat, 8, mats["gate"][:3],
+                                           mats["up"][:3], mats["down"][:3], bits=4)
+    assert np.array_equal(idx, np.tile(np.arange(8, dtype=np.uint32), (2, 1)))
+    assert np.allclose(gate, 1 / 8, atol=1e-7)
