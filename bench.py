@@ -26,7 +26,14 @@ re-targeted to HIP):
   ``roofline.frac`` is against the 8 TB/s spec and
   ``roofline.measured_ceiling`` against back-to-back probe reads of the same
   bytes per launch (each KV and MoE row carries ``frac_measured_ceiling``
-  alike).
+  alike);
+- ``valu_bound`` on every row (and on ``roofline``): min(HBM, VALU, matrix
+  core), the time the call's bytes need at 8 TB/s beside the time its
+  hardware-counted instructions need at the issue rates the compute probes
+  measure in this run (kernelverify_amd/counters.py; the counts come from
+  ``profiles/issue_counts_bench.json``, made by rocprofv3 over
+  ``--issue-profile``), the resource that binds and the achieved fraction
+  of its cap.
 
 The other BASELINE configurations ride in the same line: the qmv ones
 (config 1's 4096 x 4096, config 2's 8-bit, M = 4/8 and 4096 x 14336) under
@@ -287,6 +294,28 @@ class MoeWorkload:
         return worst
 
 
+# The rows beside the headline, in bench order.
+SECONDARY_QMV = ((4096, 4096, 4, 1), (14336, 4096, 8, 1), (14336, 4096, 4, 4),
+                 (14336, 4096, 4, 8), (4096, 14336, 4, 1))
+MOE_TOKENS = (1, 8, 32)
+
+
+def kv_rows() -> list[dict]:
+    """KvWorkload arguments: the 32k target, config 3, config 4 (seed-0 lengths)."""
+    return [dict(lengths=[32768], bits=4), dict(lengths=[8192], bits=8),
+            dict(lengths=list(np.random.default_rng(0).integers(1024, 32769, 8)), bits=4,
+                 per_sequence=True, t_stride=32768)]
+
+
+def row_factories() -> list:
+    """One constructor per bench row, headline first."""
+    rows = [lambda: QmvWorkload(14336, 4096, 4, 1)]
+    rows += [lambda c=c: QmvWorkload(*c, seed=1) for c in SECONDARY_QMV]
+    rows += [lambda kw=kw: KvWorkload(**kw) for kw in kv_rows()]
+    rows += [lambda n=n: MoeWorkload(n) for n in MOE_TOKENS]
+    return rows
+
+
 ROUNDS = 7          # replays of one K-launch graph per row (bench/interleave.py:38-103)
 SPREAD_LIMIT = 1.5  # max/min of a row's rounds above which the row is re-timed, then rejected
 MIN_SAMPLE_MS = 5.0  # the reference's floor for one timed sample (interleave.py:38)
@@ -507,6 +536,74 @@ def blas_threads() -> int:
         return int(os.environ.get("OMP_NUM_THREADS", "1"))
 
 
+ISSUE_FILE = ROOT / "profiles" / "issue_counts_bench.json"
+
+
+def issue_profile(steps: int) -> int:
+    """The program the instruction-count passes profile: every row's step
+    ``steps`` times between tag launches (kernelverify_amd/counters.py reads
+    the dispatches back by the tags), then the manifest line."""
+    from kernelverify_amd import counters, hip, lib
+
+    L = lib.load()
+    sink = hip.DeviceArray((len(row_factories()) + 1,), np.float32)
+    names = []
+    for i, make in enumerate(row_factories()):
+        w = make()
+        hip.synchronize()
+        lib.check(L.kvp_probe_compute(0, i + 1, 1, sink.ptr, None))  # open tag: row i
+        for _ in range(steps):
+            w.step(None)
+            hip.synchronize()
+        lib.check(L.kvp_probe_compute(1, 1, 1, sink.ptr, None))  # close tag
+        hip.synchronize()
+        names.append(w.name)
+        log(f"[issue] row {i}: {w.name}, {steps} steps")
+        del w
+    print(json.dumps({"issue_rows": names, "steps": steps,
+                      "kernel_source_sha256": counters.library_source_sha256()}), flush=True)
+    return 0
+
+
+class IssueBounds:
+    """min(HBM, VALU, matrix core) per row: the committed per-call
+    instruction counts (rocprofv3 over ``--issue-profile``) at the issue
+    rates the compute probes measure in this run."""
+
+    def __init__(self):
+        from kernelverify_amd import counters, roofline
+
+        self.counters = counters
+        try:
+            data = json.loads(ISSUE_FILE.read_text())
+        except (OSError, ValueError):
+            data = {"rows": {}}
+        self.rows = data.get("rows", {})
+        self.current = data.get("kernel_source_sha256") == counters.library_source_sha256()
+        c = roofline.compute_ceilings(blocks=256 * 8, iters=1024)
+        fma = c[roofline.COMPUTE_KINDS[0]]["TFLOPs"] * 1e12
+        dot2 = c[roofline.COMPUTE_KINDS[1]]["TFLOPs"] * 1e12
+        self.rates = {"valu_wave_insts_per_s": fma / (2 * 64),
+                      "dot2_wave_insts_per_s": dot2 / (4 * 64),
+                      "mfma_f16_flops_per_s": c[roofline.COMPUTE_KINDS[2]]["TFLOPs"] * 1e12}
+
+    def summary(self) -> dict:
+        return {"rates": {k: round(v / 1e9, 1) for k, v in self.rates.items()},
+                "rates_unit": "G per s (wave-instructions, flops)",
+                "counts": ISSUE_FILE.name, "counts_match_source": self.current,
+                "valu_rate_from": "fp32 FMA probe (the fastest VALU instruction measured; "
+                                  "valu_us is a lower bound)"}
+
+    def row(self, name: str, nbytes: int, achieved_GBps: float) -> dict | None:
+        work = self.counters.issue_work(self.rows.get(name, {}).get("per_call", {}))
+        if work is None:
+            return None
+        out = self.counters.issue_bound(nbytes, achieved_GBps, work, self.rates, PEAK_HBM_GBS)
+        if not self.current:
+            out["counts_stale"] = True
+        return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -517,6 +614,9 @@ def main() -> int:
                     help="skip the other BASELINE qmv configs (configs 1 and 2 beside the headline)")
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline qmv workload (profiling runs)")
+    ap.add_argument("--issue-profile", type=int, default=0, metavar="S",
+                    help="run every row S times between tag launches, for rocprofv3 counter "
+                         "passes (kernelverify_amd/counters.py); no timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
@@ -530,8 +630,10 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 3
     lib.load()
+    if args.issue_profile:
+        return issue_profile(args.issue_profile)
 
-    head = QmvWorkload(14336, 4096, 4, 1)
+    head = row_factories()[0]()
     log(f"[bench] {head.name}: {len(head.copies)} artefact copies, "
         f"{head.bytes} algorithmic bytes/launch")
 
@@ -560,6 +662,8 @@ def main() -> int:
     # reads of the headline's bytes per launch (scored against its own
     # ceiling as well as the spec).
     ceiling = None
+    bounds = IssueBounds()
+    log(f"[bench] issue rates: {bounds.summary()}")
     if not args.headline_only:
         c_gbs, c_us, c_shape = roofline.best_read_like(head.bytes)
         ceiling = {"GBps": round(c_gbs, 1), "us_per_launch": round(c_us, 3),
@@ -571,9 +675,8 @@ def main() -> int:
 
     secondary = []
     if not (args.no_secondary or args.headline_only):
-        for d_out, d_in, bits, m in ((4096, 4096, 4, 1), (14336, 4096, 8, 1), (14336, 4096, 4, 4),
-                                     (14336, 4096, 4, 8), (4096, 14336, 4, 1)):
-            w = QmvWorkload(d_out, d_in, bits, m, seed=1)
+        for c in SECONDARY_QMV:
+            w = QmvWorkload(*c, seed=1)
             g = w.gpu_output()
             r = w.cpu_reference()()
             e = float(np.max(np.abs(g.astype(np.float64) - r)))
@@ -586,14 +689,14 @@ def main() -> int:
             secondary.append({"workload": w.name, "us_per_call": round(ms2 * 1e3, 3),
                               "GBps": round(w.bytes / (ms2 * 1e-3) / 1e9, 1),
                               "frac_8TBps": round(w.bytes / (ms2 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                              "timing": t2.summary()})
+                              "timing": t2.summary(),
+                              "valu_bound": bounds.row(w.name, w.bytes,
+                                                       w.bytes / (ms2 * 1e-3) / 1e9)})
             log(f"[bench] {secondary[-1]}")
             del w
 
     kv = []
-    for kw in () if args.headline_only else (dict(lengths=[32768], bits=4), dict(lengths=[8192], bits=8),
-               dict(lengths=list(np.random.default_rng(0).integers(1024, 32769, 8)), bits=4,
-                    per_sequence=True, t_stride=32768)):
+    for kw in () if args.headline_only else kv_rows():
         w = KvWorkload(**kw)
         got = w.gpu_output()
         ratio = w.check(got)
@@ -607,6 +710,7 @@ def main() -> int:
                    "frac_8TBps": round(gbs2 / PEAK_HBM_GBS, 4), "bytes": w.bytes,
                    "verify_err_over_bound": round(ratio, 4), "timing": t2.summary()})
         kv[-1]["frac_measured_ceiling"] = round(gbs2 / roofline.best_read_like(w.bytes)[0], 4)
+        kv[-1]["valu_bound"] = bounds.row(w.name, w.bytes, gbs2)
         if not args.no_cpu:
             kv[-1]["cpu"] = cpu_row(w, got, "dequantize the stored caches, fp32 scores, "
                                     "softmax over T + 1, values (native_kernels.py:168-221)")
@@ -614,7 +718,7 @@ def main() -> int:
         del w
 
     moe_rows = []
-    for n in () if args.headline_only else (1, 8, 32):
+    for n in () if args.headline_only else MOE_TOKENS:
         w = MoeWorkload(n)
         got = w.gpu_output()
         ratio = w.check(got, tokens=(0, n - 1) if n > 1 else (0,))
@@ -629,6 +733,7 @@ def main() -> int:
                          "unique_experts": w.unique, "bytes": w.bytes,
                          "verify_err_over_bound": round(ratio, 4), "timing": t3.summary()})
         moe_rows[-1]["frac_measured_ceiling"] = round(gbs3 / roofline.best_read_like(w.bytes)[0], 4)
+        moe_rows[-1]["valu_bound"] = bounds.row(w.name, w.bytes, gbs3)
         if not args.no_cpu:
             moe_rows[-1]["cpu"] = cpu_row(w, got, "softmax top-8 routing, each routed expert's "
                                           "gate/up/down dequantized once, fp32 SwiGLU "
@@ -668,7 +773,9 @@ def main() -> int:
                    "batch": 1, "rotation_copies": len(head.copies)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "traffic": measured_traffic(), "measured_ceiling": ceiling},
+                     "traffic": measured_traffic(), "measured_ceiling": ceiling,
+                     "valu_bound": bounds.row(head.name, head.bytes, gbs),
+                     "issue_rates": bounds.summary()},
         "cpu_baseline": cpu,
     }
     if secondary:
