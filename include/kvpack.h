@@ -214,8 +214,8 @@ int kvp_moe_swiglu(const void* x, const uint32_t* idx, const float* gate,
  * else (no environment variable) changes which kernel a call runs. Keys:
  * "qmv_path" (1 streaming, 2 resident, 3 chunked, 4 matrix cores,
  * 5 persistent), "qmv_per_cu", "qmv_blocks", "qmv_kw", "qmv_rw",
- * "qmv_mfma_tiles", "moe_valu", "moe_kq", "moe_permute". value -1 restores
- * the library's choice. Process-wide; set before the calls it should
+ * "qmv_mfma_tiles", "moe_valu", "moe_kq", "moe_permute", "moe_down_combine".
+ * value -1 restores the library's choice. Process-wide; set before the calls it should
  * affect. No counterpart in the reference (its kernels have one body). */
 int kvp_set_tuning(const char* key, int value);
 int kvp_get_tuning(const char* key, int* value);

@@ -39,7 +39,7 @@ namespace {
 std::atomic<int> g_tuning[kTuneCount];
 constexpr const char* kTuneNames[kTuneCount] = {
     "qmv_path", "qmv_per_cu", "qmv_blocks", "qmv_kw", "qmv_rw", "qmv_mfma_tiles",
-    "moe_valu", "moe_kq", "moe_permute"};
+    "moe_valu", "moe_kq", "moe_permute", "moe_down_combine"};
 
 int tuning_index(const char* key) {
   for (int i = 0; key && i < kTuneCount; ++i)

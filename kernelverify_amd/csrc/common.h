@@ -48,6 +48,7 @@ enum TuneKey {
   kTuneMoeValu,        // 1: MoE experts on the VALU kernels
   kTuneMoeKq,          // matrix-core experts: 1 tile per wave, or 4 waves per tile
   kTuneMoePermute,     // 1: the separate permute launch even where in-block routing applies
+  kTuneMoeDownCombine, // SwiGLU down projection: 1 fused with the gated sum, 0 the two launches
   kTuneCount
 };
 int tuning(TuneKey key, int fallback);

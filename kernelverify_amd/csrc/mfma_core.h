@@ -34,9 +34,6 @@ struct MfmaShape {
   static constexpr int kWPL = kCPL * BITS / 32;  // code words per lane per step
   static constexpr int kGroupBytes = 8 * BITS;   // one 64-code group of a row
   static constexpr int kSlotsPerGroup = 9;       // 8 slots of 8 codes + 1 pad slot (banks)
-  // Steps in flight per wave: about 4 KiB of weights per wave (deeper rings
-  // cost the VGPRs that let two 8-wave blocks share a CU).
-  static constexpr int kPD = (4096 / (64 * kWPL * 4)) < 2 ? 2 : 4096 / (64 * kWPL * 4);
 };
 
 // Pair order of one 8-code slot: operand position p holds x[slot_src(p)].

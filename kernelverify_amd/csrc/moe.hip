@@ -40,35 +40,6 @@ constexpr int kPermuteTile = 8192;  // routed pairs (n * k) one permutation hold
 // ---------------------------------------------------------------------------
 // Routing
 // ---------------------------------------------------------------------------
-// Wave-wide argmax by (value desc, index asc): the winner every lane agrees
-// on. The order is total, so any pairing of lanes reaches it: DPP steps
-// within each 16-lane row, then the four row winners read as scalars.
-__device__ __forceinline__ void take_better(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) {
-    v = ov;
-    i = oi;
-  }
-}
-template <int CTRL>
-__device__ __forceinline__ void argmax_step(float& v, int& i) {
-  take_better(v, i, dpp_f<CTRL>(v), dpp_i<CTRL>(i));
-}
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-  argmax_step<kQuadSwap1>(v, i);
-  argmax_step<kQuadSwap2>(v, i);
-  argmax_step<kHalfMirror>(v, i);
-  argmax_step<kRowMirror>(v, i);
-  const int vb = __builtin_bit_cast(int, v);
-  float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vb, 0));
-  int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-  for (int row = 16; row < kWave; row += 16)
-    take_better(bv, bi, __builtin_bit_cast(float, __builtin_amdgcn_readlane(vb, row)),
-                __builtin_amdgcn_readlane(i, row));
-  v = bv;
-  i = bi;
-}
-
 // logits: E fp32 values of one token, held as E/64 per lane (lane-strided).
 template <int EPL>
 __device__ __forceinline__ void route_token(const float (&lg)[EPL], int n_experts, int k,
@@ -91,38 +62,39 @@ __device__ __forceinline__ void route_token(const float (&lg)[EPL], int n_expert
   float p[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) p[j] = (lane + j * kWave < n_experts) ? e[j] / denom : -1.0f;
-  // k rounds of a wave argmax; the chosen expert is knocked out (-inf).
-  float chosen_p[kMaxK];
-  int chosen_i[kMaxK];
+  // k rounds: the largest p (a wave max), then the lowest expert index
+  // holding it (ballots, lane-strided index order), knocked out (-inf).
+  // Lane s keeps slot s; the renormalising sum runs in slot order.
+  float my_p = 0.0f;
+  int my_i = 0;
   float total = 0.0f;
-  for (int s = 0; s < k; ++s) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+  for (int s = 0; s < k; ++s) {  // wave-uniform
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) m = fmaxf(m, p[j]);
+    m = wave_max(m);
+    int bi = -1;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
-      const int ei = lane + j * kWave;
-      if (p[j] > bv || (p[j] == bv && ei < bi)) {
-        bv = p[j];
-        bi = ei;
-      }
+      const unsigned long long hit = __ballot(p[j] == m);
+      if (bi < 0 && hit != 0ull) bi = j * kWave + __ffsll((long long)hit) - 1;
     }
-    wave_argmax(bv, bi);
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
       if (lane + j * kWave == bi) p[j] = -INFINITY;
-    chosen_p[s] = bv;
-    chosen_i[s] = bi;
+    if (lane == s) {
+      my_p = m;
+      my_i = bi;
+    }
+    total += m;
   }
-  // Renormalise over the k chosen, summed in slot order.
-  for (int s = 0; s < k; ++s) total += chosen_p[s];
-  if (lane == 0) {
-    for (int s = 0; s < k; ++s) {
-      idx[s] = (uint32_t)chosen_i[s];
-      gate[s] = chosen_p[s] / total;
-      if (idx2) {
-        idx2[s] = (uint32_t)chosen_i[s];
-        gate2[s] = chosen_p[s] / total;
-      }
+  if (lane < k) {
+    const float g = my_p / total;
+    idx[lane] = (uint32_t)my_i;
+    gate[lane] = g;
+    if (idx2) {
+      idx2[lane] = (uint32_t)my_i;
+      gate2[lane] = g;
     }
   }
 }
@@ -907,6 +879,192 @@ __global__ __launch_bounds__(kBlock) void scatter_kernel(const float* __restrict
   store_out<OutT>(out + i, acc);
 }
 
+// Down projection and the gated sum in one launch, for a few tokens. A
+// block is one 16-row tile of the output for one token; wave w takes the
+// token's slots w, w + kDcWaves, ...: it stages the slot's hidden state as
+// fp16 hi/lo rows (the down launch's split, h * 2^-E = hi + lo), walks its
+// expert's tile on the matrix cores exactly as the down launch does (the
+// same steps in the same order, so y_s is the same fp32 value) and leaves
+// y_s in LDS; the block then forms out = sum_s gate_s * y_s in slot order,
+// the scatter kernel's sum. Each token reads its experts' tiles itself, so
+// this serves token counts whose routed experts barely repeat.
+constexpr int kDcWaves = 8;
+
+struct DownCombineArgs {
+  const float* h;          // [pairs][d_in] fp32 hidden states, sorted pair order
+  const int32_t* slot_of;  // [n][k]: row of h for (t, s), or -1
+  const uint32_t* idx;     // [n][k] experts
+  const float* gate;       // [n][k]
+  const uint32_t* wq;      // [E][d_out][d_in*bits/32]
+  const uint16_t* s;
+  const uint16_t* b;
+  void* out;               // [n][d_out]
+  int k, n_experts, d_in, d_out;
+};
+
+// LDS bytes of one wave's staging (hi and lo rows, zero slots, sums, shifts).
+__host__ __device__ constexpr size_t dc_wave_bytes(int G) {
+  return (size_t)(2 * (G * kEGroupSlots + 1) + 8) * 16 + (size_t)G * kEMT * 8;
+}
+
+template <int BITS, typename OutT>
+__global__ __launch_bounds__(64 * kDcWaves) void down_combine_kernel(DownCombineArgs a) {
+  using S = MfmaShape<BITS, kEMT>;
+  constexpr int RS = 4;  // steps in flight per wave
+  extern __shared__ __align__(16) uint4 lds[];
+  __shared__ float ys[kMaxK][16];
+  __shared__ int valid[kMaxK];
+  const int G = a.d_in / 64;  // a multiple of 4 (checked by the launcher)
+  const int steps = G / S::kNB;
+  const int m_stride = G * kEGroupSlots + 1;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int t = blockIdx.y;
+  uint4* xs = lds + wave * (dc_wave_bytes(G) / 16);  // rows 0 (hi) and 1 (lo)
+  uint4* zeros = xs + 2 * m_stride;
+  float* sums = reinterpret_cast<float*>(zeros + 8);  // [G][kEMT]
+  float* mult = sums + G * kEMT;                       // [G][kEMT]
+  if (lane < S::kT) zeros[lane] = uint4{0, 0, 0, 0};
+
+  const int n = lane & 15, hq = lane >> 4;  // weight row in the tile; k-octet and row block
+  const int row = blockIdx.x * 16 + n;
+  const bool row_ok = row < a.d_out;
+  const uint32_t row_bytes = (uint32_t)a.d_in * BITS / 8;
+  const uint32_t code_base = row_ok ? (uint32_t)row * row_bytes + hq * S::kGroupBytes : kOutOfRange;
+  const uint32_t sb_base = row_ok ? ((uint32_t)row * G + hq) * 2 : kOutOfRange;
+  // A row n is (block n / 4, row n % 4): rows 0 and 1 hold hi and lo, 2 and
+  // 3 read the zero slots.
+  const bool a_live = (n >> 2) == hq && (n & 3) < 2;
+  const uint4* a_base = a_live ? xs + (n & 3) * m_stride + hq * kEGroupSlots : zeros;
+  const uint32_t a_mul = a_live ? 1u : 0u;
+  const uint32_t wbytes = (uint32_t)(a.d_out * row_bytes), sbytes = (uint32_t)(a.d_out * G * 2);
+
+  for (int sl = wave; sl < a.k; sl += kDcWaves) {  // wave-uniform
+    const int pair = t * a.k + sl;
+    const uint32_t e = a.idx[pair];
+    const int hrow = a.slot_of[pair];
+    const bool use = e < (uint32_t)a.n_experts && hrow >= 0;  // wave-uniform
+    if (lane == 0) valid[sl] = use ? 1 : 0;
+    if (!use) continue;
+    const size_t erow = (size_t)e * a.d_out;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.wq + erow * (row_bytes / 4), wbytes);
+    const __amdgpu_buffer_rsrc_t sr = rsrc(a.s + erow * G, sbytes);
+    const __amdgpu_buffer_rsrc_t br = rsrc(a.b + erow * G, sbytes);
+    ExpertStep<BITS, false> R[RS];
+    auto load = [&](ExpertStep<BITS, false>& Rs, int st) {
+      const bool live = st < steps;  // wave-uniform
+      const uint32_t co = code_base + (live ? (uint32_t)st * 4 * S::kGroupBytes : kOutOfRange);
+      const uint32_t so = sb_base + (live ? (uint32_t)st * 4 * 2 : kOutOfRange);
+#pragma unroll
+      for (int i = 0; i < S::kWPL; i += 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, co + 4 * i, 0, 0);
+        Rs.w[0][i] = v.x; Rs.w[0][i + 1] = v.y; Rs.w[0][i + 2] = v.z; Rs.w[0][i + 3] = v.w;
+      }
+      Rs.s[0] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
+      Rs.b[0] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+    };
+#pragma unroll
+    for (int j = 0; j < RS; ++j) load(R[j], j);
+
+    // Stage: item (group, quarter of 16 values); the four lanes of a group
+    // agree on its shift (the largest |h| of the group below 2^14).
+    __builtin_amdgcn_wave_barrier();  // the previous slot's operand reads come first
+    for (int it = lane; it < 4 * G; it += kWave) {
+      const int qq = it & 3, g = it >> 2;
+      const float* src = a.h + (size_t)hrow * a.d_in + g * 64 + 16 * qq;
+      float hv[16];
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(src + i);
+        hv[i] = v.x; hv[i + 1] = v.y; hv[i + 2] = v.z; hv[i + 3] = v.w;
+      }
+      float mx = 0.0f, tot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        mx = fmaxf(mx, fabsf(hv[i]));
+        tot += hv[i];
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 1, 4));
+      mx = fmaxf(mx, __shfl_xor(mx, 2, 4));
+      tot += __shfl_xor(tot, 1, 4);
+      tot += __shfl_xor(tot, 2, 4);
+      const int ex = mx > 0.0f ? max(0, ilogbf(mx) - 13) : 0;
+      const float inv = ldexpf(1.0f, -ex);
+      uint4* dhi = xs + g * kEGroupSlots + 2 * qq;
+      uint4* dlo = dhi + m_stride;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        f16x8 hi8, lo8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float hs = hv[8 * q + j] * inv;
+          const _Float16 hi = (_Float16)hs;
+          hi8[j] = hi;
+          lo8[j] = (_Float16)(hs - (float)hi);
+        }
+        const u32x4 oh = to_slot_order<BITS>(__builtin_bit_cast(u32x4, hi8));
+        const u32x4 ol = to_slot_order<BITS>(__builtin_bit_cast(u32x4, lo8));
+        dhi[q] = uint4{oh.x, oh.y, oh.z, oh.w};
+        dlo[q] = uint4{ol.x, ol.y, ol.z, ol.w};
+      }
+      if (qq == 0) {  // b * sum(h) rides on the hi row; both rows scale back by 2^E
+        const f32x4 sm = {tot, 0.0f, 0.0f, 0.0f};
+        const float m2 = ldexpf(1.0f, ex);
+        const f32x4 mu = {m2, m2, 1.0f, 1.0f};
+        *reinterpret_cast<f32x4*>(sums + g * kEMT) = sm;
+        *reinterpret_cast<f32x4*>(mult + g * kEMT) = mu;
+      }
+    }
+    // The rows written above are read below by other lanes of this wave: a
+    // wave's LDS operations run in program order, so holding the compiler
+    // at this point is enough.
+    __builtin_amdgcn_wave_barrier();
+
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int jb = 0; jb < steps; jb += RS) {  // wave-uniform
+      if (jb > 0) {
+#pragma unroll
+        for (int j = 0; j < RS; ++j) load(R[j], jb + j);
+      }
+#pragma unroll
+      for (int j = 0; j < RS; ++j) {
+        const int st = jb + j;
+        if (st < steps) {
+          const int g = st * S::kNB + hq;
+          const uint4* a_src = a_base + a_mul * (uint32_t)(st * S::kNB * kEGroupSlots);
+          const f32x4 sm = *reinterpret_cast<const f32x4*>(sums + g * kEMT);
+          const f32x4 mu = *reinterpret_cast<const f32x4*>(mult + g * kEMT);
+          f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int tt = 0; tt < S::kT; ++tt)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_src[tt]),
+                                                       code_operand<BITS>(R[j].w[0], tt), d, 0, 0,
+                                                       0);
+          const float sc = f16_bits_to_f32((uint16_t)R[j].s[0]) * 16777216.0f;  // c * 2^-24
+          const float bi = f16_bits_to_f32((uint16_t)R[j].b[0]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc * mu[r], d[r], fmaf(bi, sm[r], acc[r]));
+        }
+      }
+    }
+    // Merge the four row blocks (other groups, same A rows): y_s = hi + lo.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc[r] += __shfl_xor(acc[r], 16);
+      acc[r] += __shfl_xor(acc[r], 32);
+    }
+    if (lane < 16) ys[sl][n] = acc[0] + acc[1];
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int orow = blockIdx.x * 16 + threadIdx.x;
+    float v = 0.0f;
+    for (int sl = 0; sl < a.k; ++sl)
+      if (valid[sl]) v = fmaf(a.gate[t * a.k + sl], ys[sl][threadIdx.x], v);
+    if (orow < a.d_out) store_out<OutT>(static_cast<OutT*>(a.out) + (size_t)t * a.d_out + orow, v);
+  }
+}
+
 // Single-linear dispatch, the reference's contract at any k
 // (kernelverify/pack/moe_dispatch.py:84-138): one block per (token, rows);
 // for each slot in order, the rows of that slot's expert against the
@@ -1067,6 +1225,30 @@ int launch_experts_bits(int bits, const ExpertArgs& a, int max_active, bool swig
     case 8: return launch_experts<8>(a, max_active, swiglu, f32_in, st);
   }
   return set_error(KVP_UNSUPPORTED, "kvp_moe: bits=%d not in {2,3,4,8}", bits);
+}
+
+// Tokens up to which the SwiGLU call fuses the down projection with the
+// gated sum (tuning key moe_down_combine overrides): every token then reads
+// its own experts' down tiles. Measured on MI355X, config 5 (128 experts,
+// top-8, 2048 / 768, 4-bit), fused against the down launch + scatter:
+// n = 1 21.2 / 23.9 us, 2 24.3 / 27.9, 4 37.1 / 41.2, 8 55.8 / 57.6, and
+// 32 140.3 / 111.0 (the repeated expert reads then dominate).
+constexpr int kDownCombineTokens = 8;
+
+int launch_down_combine(int bits, int out_dtype, const DownCombineArgs& c, int n,
+                        hipStream_t st) {
+  const int G = c.d_in / 64;
+  const size_t lds = (size_t)kDcWaves * dc_wave_bytes(G);
+  const dim3 grid((c.d_out + 15) / 16, n);
+  const dim3 block(64 * kDcWaves);
+#define KVP_DC(B, T) hipLaunchKernelGGL((down_combine_kernel<B, T>), grid, block, lds, st, c)
+  if (bits == 4) {
+    if (out_dtype == KVP_F16) KVP_DC(4, f16); else KVP_DC(4, float);
+  } else {
+    if (out_dtype == KVP_F16) KVP_DC(8, f16); else KVP_DC(8, float);
+  }
+#undef KVP_DC
+  return check_launch("kvp_moe down projection + gated sum");
 }
 
 int launch_scatter(const float* y, const int32_t* slot_of, const float* gate, void* out,
@@ -1262,6 +1444,28 @@ int swiglu_impl(const char* who, const float* logits, const void* x, uint32_t* i
     a.t_slot_of = slot_of;
   }
   if (int rc = launch_experts_bits(bits, a, max_active, true, false, st)) return rc;
+
+  // A few tokens: the down projection and the gated sum in one launch.
+  const int G_dn = d_ffn / 64;
+  const bool dc_fits = (bits == 4 || bits == 8) && mfma_experts(bits, d_ffn) &&
+                       (size_t)kDcWaves * dc_wave_bytes(G_dn) <= 64 * 1024;
+  const int dc = tuning(kTuneMoeDownCombine, n <= kDownCombineTokens ? 1 : 0);
+  if (dc_fits && dc == 1) {
+    DownCombineArgs c{};
+    c.h = h;
+    c.slot_of = slot_of;
+    c.idx = idx;
+    c.gate = gate;
+    c.wq = down_wq;
+    c.s = static_cast<const uint16_t*>(down_scales);
+    c.b = static_cast<const uint16_t*>(down_biases);
+    c.out = out;
+    c.k = k;
+    c.n_experts = n_experts;
+    c.d_in = d_ffn;
+    c.d_out = d_model;
+    return launch_down_combine(bits, out_dtype, c, n, st);
+  }
 
   ExpertArgs dn{};
   dn.xf = h;

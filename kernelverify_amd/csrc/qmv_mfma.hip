@@ -32,7 +32,11 @@
 namespace kvp {
 namespace {
 
-constexpr int kMfmaStageBytes = 64 * 1024;  // x chunk budget per block
+// x chunk budget per block: the whole row of x for M <= 8 at 4096 codes
+// (77 KB at M = 8), so those run as one chunk with no hand-off barriers
+// (measured, 14336 x 4096 M = 8: 17.0 us against 21.5 with a 64 KB budget);
+// clamped to what the device lets a block allocate.
+constexpr int kMfmaStageBytes = 96 * 1024;
 
 template <int BITS, int MT>
 struct MfmaStep {
@@ -77,18 +81,17 @@ __device__ __forceinline__ void mfma_commit(const u32x4 (&v)[8], int M, int kc, 
 }
 
 // A block is TB row tiles of 16 rows; each tile's steps are split over KQ
-// waves. A wave runs its steps through a ring of kPD register sets, so kPD
+// waves. A wave runs its steps through a ring of PD register sets, so PD
 // steps of weight loads are in flight while it computes. Every per-step
 // address is a per-lane base plus one wave-uniform offset (the buffer
 // loads' scalar offset), so a step costs no index arithmetic on the VALU.
-template <int BITS, int MT, int TB, int KQ, typename OutT>
+template <int BITS, int MT, int TB, int KQ, int PD, typename OutT>
 __global__ __launch_bounds__(64 * TB * KQ) void qmv_mfma_kernel(
     const f16* __restrict__ x, const uint32_t* __restrict__ wq,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     OutT* __restrict__ out, int M, int d_in, int d_out, int kc) {
   using S = MfmaShape<BITS, MT>;
   constexpr int W = TB * KQ;
-  constexpr int PD = S::kPD;
   constexpr int kGroupSlots = S::kSlotsPerGroup;
   extern __shared__ __align__(16) uint4 lds[];
   __shared__ float red[W][16][16];
@@ -227,6 +230,38 @@ __global__ __launch_bounds__(64 * TB * KQ) void qmv_mfma_kernel(
   }
 }
 
+// Dynamic LDS a block may take on this device besides `static_bytes`.
+inline int stage_budget(int static_bytes) {
+  static thread_local int max_block = 0;
+  if (max_block == 0) {
+    int dev = 0, v = 0;
+    hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        v <= 0)
+      v = 64 * 1024;
+    max_block = v;
+  }
+  return min(kMfmaStageBytes, max_block - static_bytes);
+}
+
+// Ring depth (steps of weight loads in flight per wave) for code words per
+// lane and step `wpl`: about 4 KiB of weights per wave. Deeper rings
+// (every step of a chunk in flight) measured slower on MI355X at M = 2 to 8:
+// their VGPRs cost co-resident waves (4096 x 4096 M = 2: 8.5 against 6.2 us).
+constexpr int ring_depth(int wpl) { return 16 / wpl < 2 ? 2 : 16 / wpl; }
+
+template <int BITS, int MT, int TB, int KQ, int PD, typename OutT>
+int launch_pd(const void* x, const uint32_t* wq, const void* s, const void* b, void* out, int m,
+              int d_out, int d_in, int kc, size_t lds, hipStream_t stream) {
+  const int tiles = (d_out + 15) / 16;
+  const int blocks = (tiles + TB - 1) / TB;
+  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, MT, TB, KQ, PD, OutT>), dim3(blocks),
+                     dim3(64 * TB * KQ), lds, stream, static_cast<const f16*>(x), wq,
+                     static_cast<const uint16_t*>(s), static_cast<const uint16_t*>(b),
+                     static_cast<OutT*>(out), m, d_in, d_out, kc);
+  return check_launch("kvp_qmv (matrix cores)");
+}
+
 template <int BITS, int MT, int TB, int KQ, typename OutT>
 int launch_mt(const void* x, const uint32_t* wq, const void* s, const void* b, void* out, int m,
               int d_out, int d_in, hipStream_t stream) {
@@ -235,19 +270,16 @@ int launch_mt(const void* x, const uint32_t* wq, const void* s, const void* b, v
   // Groups per staged chunk: the LDS budget over (x rows x 9 slots + 16 sums),
   // a whole number of steps, at most the row.
   const int per_group = m * S::kSlotsPerGroup * 16 + 16 * 4;
-  int kc = (kMfmaStageBytes - (m + S::kT) * 16) / per_group;
+  const int budget = stage_budget(TB * KQ * 16 * 16 * 4);  // the merge buffer is static
+  int kc = (budget - (m + S::kT) * 16) / per_group;
   kc = min(kc, 64 * TB * KQ / MT);  // one staging item per thread
   kc = kc / (S::kNB * KQ) * (S::kNB * KQ);
   if (kc < S::kNB * KQ) kc = S::kNB * KQ;
   const int g_pad = (G + S::kNB - 1) / S::kNB * S::kNB;
   if (kc > g_pad) kc = g_pad;
   const size_t lds = ((size_t)m * (kc * S::kSlotsPerGroup + 1) + S::kT) * 16 + (size_t)kc * 16 * 4;
-  const int tiles = (d_out + 15) / 16;
-  const int blocks = (tiles + TB - 1) / TB;
-  hipLaunchKernelGGL((qmv_mfma_kernel<BITS, MT, TB, KQ, OutT>), dim3(blocks), dim3(64 * TB * KQ),
-                     lds, stream, static_cast<const f16*>(x), wq, static_cast<const uint16_t*>(s),
-                     static_cast<const uint16_t*>(b), static_cast<OutT*>(out), m, d_in, d_out, kc);
-  return check_launch("kvp_qmv (matrix cores)");
+  return launch_pd<BITS, MT, TB, KQ, ring_depth(S::kWPL), OutT>(
+      x, wq, s, b, out, m, d_out, d_in, kc, lds, stream);
 }
 
 template <int BITS, int MT, typename OutT>

@@ -327,6 +327,46 @@ def test_in_block_routing_equals_the_permute_launch(bits):
     assert v.ok, v
 
 
+@pytest.mark.parametrize("n,e,k,d_model,d_ffn,bits,scale", [
+    (1, 128, 8, 2048, 768, 4, 1.0),    # config 5, the fused path's own case
+    (3, 16, 4, 512, 256, 8, 1.0),
+    (2, 32, 12, 512, 1024, 4, 1.0),    # k > 8: two slots on some waves
+    (2, 16, 4, 512, 1280, 4, 1.0),     # 5 steps: two rounds of weight loads
+    (4, 16, 4, 512, 256, 4, 600.0),    # hidden states beyond fp16 range
+])
+def test_down_combine_equals_the_two_launches(n, e, k, d_model, d_ffn, bits, scale):
+    """The down projection fused with the gated sum (tuning key
+    moe_down_combine = 1) is bit-identical to the down launch followed by
+    the scatter (= 0) when that launch walks each tile's steps in one wave
+    (moe_kq = 1, as the fused kernel does): the same fp32 y_s, summed in
+    slot order. Also with a slot naming no expert and with none valid; fp16
+    and fp32 outputs; the fused output against the oracle."""
+    x, mats, logits = swiglu_case(n, e, d_model, d_ffn, bits, seed=90 + n + k)
+    x = (x.astype(np.float32) * scale).astype(np.float16)
+    idx, gate = route_topk(logits, k)
+    idx = idx.astype(np.uint32)
+    bad = idx.copy()
+    bad[n - 1, 1] = e
+    none = np.full_like(idx, e + 5)
+    try:
+        lib.set_tuning("moe_kq", 1)
+        for name, ids in (("routed", idx), ("one-invalid", bad), ("none-valid", none)):
+            for dtype in ("float16", "float32"):
+                lib.set_tuning("moe_down_combine", 1)
+                fused = run_swiglu(x, mats, ids, gate, bits, dtype)
+                lib.set_tuning("moe_down_combine", 0)
+                separate = run_swiglu(x, mats, ids, gate, bits, dtype)
+                assert np.array_equal(fused, separate), (name, dtype)
+                if name == "none-valid":
+                    assert not np.any(fused)
+                elif name == "routed" and dtype == "float32":
+                    v = judge_swiglu(x, mats, idx, gate, fused, [0, n - 1], "float32")
+                    assert v.ok, v
+    finally:
+        lib.set_tuning("moe_down_combine", -1)
+        lib.set_tuning("moe_kq", -1)
+
+
 @pytest.mark.parametrize("n", [64, 65])
 def test_in_block_routing_limit(n):
     """n * k = 512 pairs is the largest in-block routing (bit-identical to
