@@ -28,6 +28,7 @@
 
 namespace kvp {
 
+bool qmv_mfma_fits(int bits);
 int launch_qmv_mfma(int bits, bool f32_out, const void* x, const uint32_t* wq, const void* s,
                     const void* b, void* out, int m, int d_out, int d_in, hipStream_t st);
 
@@ -895,14 +896,21 @@ int launch_qmv_rw(const void* x, const uint32_t* wq, const void* scales, const v
   }
 }
 
+// The VALU kernels hold at most 8 rows of x (their accumulators and
+// staged activations for more rows spill to scratch on gfx950): M = 9..16
+// runs as two calls over rows 0..7 and 8..M-1, each reading the weights.
 template <int BITS, typename OutT>
 int dispatch_m(int m, const void* x, const uint32_t* wq, const void* s, const void* b, void* out,
                int d_out, int d_in, hipStream_t st) {
+  if (m > 8) {
+    if (int rc = dispatch_m<BITS, OutT>(8, x, wq, s, b, out, d_out, d_in, st)) return rc;
+    return dispatch_m<BITS, OutT>(m - 8, static_cast<const f16*>(x) + (size_t)8 * d_in, wq, s, b,
+                                  static_cast<OutT*>(out) + (size_t)8 * d_out, d_out, d_in, st);
+  }
   switch (m) {
 #define KVP_M(N) \
   case N: return launch_qmv_rw<BITS, N, OutT>(x, wq, s, b, out, d_out, d_in, st);
     KVP_M(1) KVP_M(2) KVP_M(3) KVP_M(4) KVP_M(5) KVP_M(6) KVP_M(7) KVP_M(8)
-    KVP_M(9) KVP_M(10) KVP_M(11) KVP_M(12) KVP_M(13) KVP_M(14) KVP_M(15) KVP_M(16)
 #undef KVP_M
   }
   return set_error(KVP_INVALID, "kvp_qmv: m=%d outside 1..16", m);
@@ -911,15 +919,17 @@ int dispatch_m(int m, const void* x, const uint32_t* wq, const void* s, const vo
 template <typename OutT>
 int dispatch_bits(int bits, int m, const void* x, const uint32_t* wq, const void* s,
                   const void* b, void* out, int d_out, int d_in, hipStream_t st) {
-  // Matrix cores for 4/8-bit at M >= 2 (qmv_mfma.hip): their cost does not
-  // grow with M. At M = 2 over rows of at most 4096 codes the VALU paths are
-  // still as fast or faster (measured on MI355X: 14336 x 4096 11.4 against
-  // 12.2 us, 4096 x 4096 5.9 against 6.2). qmv_path = 4 forces the matrix
-  // cores, 1..3 the VALU paths.
+  // Matrix cores at M >= 2 (qmv_mfma.hip): their cost does not grow with M.
+  // At 4 and 8 bits and M = 2 over rows of at most 4096 codes the VALU paths
+  // are still as fast or faster (measured on MI355X, 4-bit: 14336 x 4096 11.4
+  // against 12.2 us, 4096 x 4096 5.9 against 6.2); at 2 and 3 bits the
+  // matrix cores win from M = 2 (3-bit 14336 x 4096: 12.1 against 18.3).
+  // qmv_path = 4 forces the matrix cores where they fit, 1..3 the VALU paths.
   const int path = tuning(kTuneQmvPath, 0);
-  const bool fits = (size_t)d_out * d_in / 8 * bits < (size_t(1) << 31);  // 32-bit buffer offsets
-  const bool mfma_auto = m >= 3 || (m == 2 && d_in > 4096);
-  if ((bits == 4 || bits == 8) && fits && ((path == 0 && mfma_auto) || path == 4))
+  const bool fits = (size_t)d_out * d_in / 8 * bits < (size_t(1) << 31) &&  // 32-bit offsets
+                    qmv_mfma_fits(bits);
+  const bool mfma_auto = m >= 3 || (m == 2 && (bits <= 3 || d_in > 4096));
+  if (fits && ((path == 0 && mfma_auto) || path == 4))
     return launch_qmv_mfma(bits, sizeof(OutT) == 4, x, wq, s, b, out, m, d_out, d_in, st);
   switch (bits) {
     case 2: return dispatch_m<2, OutT>(m, x, wq, s, b, out, d_out, d_in, st);

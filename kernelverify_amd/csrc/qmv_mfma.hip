@@ -1,6 +1,6 @@
 // Affine group-quantized matvec on the matrix cores, for M = 2..16 rows of x
-// (4- and 8-bit codes). Same operator and contract as qmv.hip
-// (reference kv_wide_qmv, kernelverify/pack/wide_qmv.py:65-135): per 64-code
+// (2-, 3-, 4- and 8-bit codes). Same operator and contract as
+// qmv.hip (reference kv_wide_qmv, kernelverify/pack/wide_qmv.py:65-135): per 64-code
 // group s * dot(x, q) + b * sum(x), fp32 accumulation, one weight pass.
 //
 // Why a second kernel: the VALU path spends one V_DOT2 per code pair per row
@@ -70,9 +70,11 @@ __device__ __forceinline__ void mfma_commit(const u32x4 (&v)[8], int M, int kc, 
   const int m = it / kc, gl = it - m * kc;
   float sum = 0.0f;
   uint4* dst = xs + min(m, M - 1) * m_stride_slots + gl * MfmaShape<BITS, MT>::kSlotsPerGroup;
+  u32x4 op[8];
+  group_slot_order<BITS>(v, op);
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
-    const u32x4 ow = to_slot_order<BITS>(v[q]);
+    const u32x4 ow = op[q];
 #pragma unroll
     for (int j = 0; j < 4; ++j) sum = dot2(ow[j], 0x3C003C00u, sum);
     if (m < M) dst[q] = uint4{ow.x, ow.y, ow.z, ow.w};
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(64 * TB * KQ) void qmv_mfma_kernel(
   // Per-lane bases; a step adds the wave-uniform group of its block 0.
   const bool row_ok = row < d_out;
   const uint32_t code_base =
-      row_ok ? (uint32_t)row * row_bytes + blk * S::kGroupBytes + share * (S::kWPL * 4)
+      row_ok ? (uint32_t)row * row_bytes + blk * S::kGroupBytes + share * S::kShareBytes
              : kOutOfRange;
   const uint32_t sb_base = row_ok ? ((uint32_t)row * G + blk) * 2 : kOutOfRange;
   // A side: this lane's x row and whether its row block matches its octet.
@@ -143,9 +145,25 @@ __global__ __launch_bounds__(64 * TB * KQ) void qmv_mfma_kernel(
     // The whole offset goes in the range-checked VGPR offset (never the
     // scalar one): a dead step or row lands past the buffer and reads zeros.
     const uint32_t co = code_base + co_s, sbo = sb_base + sb_s;
-    if constexpr (S::kWPL == 2) {
+    if constexpr (S::kShareBytes == 6) {  // 3-bit, a quarter group: 2-byte aligned
+      const uint32_t h0 = __builtin_amdgcn_raw_buffer_load_b16(wr, co, 0, 0);
+      const uint32_t h1 = __builtin_amdgcn_raw_buffer_load_b16(wr, co + 2, 0, 0);
+      R.w[1] = __builtin_amdgcn_raw_buffer_load_b16(wr, co + 4, 0, 0);
+      R.w[0] = h0 | (h1 << 16);
+    } else if constexpr (S::kWPL == 1) {
+      R.w[0] = __builtin_amdgcn_raw_buffer_load_b32(wr, co, 0, 0);
+    } else if constexpr (S::kWPL == 2) {
       const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(wr, co, 0, 0);
       R.w[0] = v.x; R.w[1] = v.y;
+    } else if constexpr (S::kWPL == 3) {  // 3-bit, half a group: 4-byte aligned
+#pragma unroll
+      for (int i = 0; i < 3; ++i) R.w[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, co + 4 * i, 0, 0);
+    } else if constexpr (S::kWPL == 6) {  // 3-bit, a whole group: 8-byte aligned
+#pragma unroll
+      for (int i = 0; i < 6; i += 2) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(wr, co + 4 * i, 0, 0);
+        R.w[i] = v.x; R.w[i + 1] = v.y;
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < S::kWPL; i += 4) {
@@ -312,15 +330,21 @@ int launch_bits(const void* x, const uint32_t* wq, const void* s, const void* b,
 
 }  // namespace
 
-// Host entry used by kvp_qmv's dispatcher (qmv.hip) for 4/8-bit, M >= 2.
+// Whether the matrix-core kernel takes this width.
+bool qmv_mfma_fits(int bits) { return bits == 2 || bits == 3 || bits == 4 || bits == 8; }
+
+// Host entry used by kvp_qmv's dispatcher (qmv.hip) at M >= 2.
 int launch_qmv_mfma(int bits, bool f32_out, const void* x, const uint32_t* wq, const void* s,
                     const void* b, void* out, int m, int d_out, int d_in, hipStream_t st) {
-  if (bits == 4) {
-    return f32_out ? launch_bits<4, float>(x, wq, s, b, out, m, d_out, d_in, st)
-                   : launch_bits<4, f16>(x, wq, s, b, out, m, d_out, d_in, st);
+  switch (bits) {
+#define KVP_BITS(B)                                                                           \
+  case B:                                                                                     \
+    return f32_out ? launch_bits<B, float>(x, wq, s, b, out, m, d_out, d_in, st)             \
+                   : launch_bits<B, f16>(x, wq, s, b, out, m, d_out, d_in, st);
+    KVP_BITS(2) KVP_BITS(3) KVP_BITS(4) KVP_BITS(8)
+#undef KVP_BITS
   }
-  return f32_out ? launch_bits<8, float>(x, wq, s, b, out, m, d_out, d_in, st)
-                 : launch_bits<8, f16>(x, wq, s, b, out, m, d_out, d_in, st);
+  return set_error(KVP_UNSUPPORTED, "kvp_qmv (matrix cores): bits=%d", bits);
 }
 
 }  // namespace kvp

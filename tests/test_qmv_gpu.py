@@ -63,6 +63,46 @@ def test_every_width_and_m(bits, m):
         assert v.ok, (bits, m, out_dtype, v)
 
 
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 8, 9, 16])
+@pytest.mark.parametrize("d_out,d_in", [(300, 1024), (77, 384), (40, 320)])
+def test_matrix_cores_at_two_and_three_bits(bits, m, d_out, d_in):
+    """The matrix-core kernel forced (tuning key qmv_path = 4) at 2 and 3
+    bits: four, two or one group per step (M <= 4, <= 8 with an even group
+    count, otherwise; a 3-bit lane then holds 48 bits of a group, loaded as
+    three halfwords), judged against the oracle on all rows."""
+    from kernelverify_amd import lib
+
+    x, q, s, b = draw_qmv(d_out, d_in, bits, m, seed=500 + 13 * bits + m + d_in)
+    art = artefact_from_arrays(q, s, b, bits)
+    lib.set_tuning("qmv_path", 4)
+    try:
+        got = run_gpu(x, art, bits, "float32")
+    finally:
+        lib.set_tuning("qmv_path", -1)
+    v = gate(x, art, got, "float32")
+    assert v.ok, (bits, m, d_out, d_in, v)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("m", [9, 16])
+def test_valu_kernels_above_eight_rows(bits, m):
+    """The VALU kernels forced (tuning key qmv_path = 3, chunked x) at M = 9
+    and 16: the library runs them as two calls of at most eight rows of x
+    (rows 8.. offset into x and out), judged against the oracle."""
+    from kernelverify_amd import lib
+
+    x, q, s, b = draw_qmv(200, 1024, bits, m, seed=700 + 11 * bits + m)
+    art = artefact_from_arrays(q, s, b, bits)
+    lib.set_tuning("qmv_path", 3)
+    try:
+        got = run_gpu(x, art, bits, "float32")
+    finally:
+        lib.set_tuning("qmv_path", -1)
+    v = gate(x, art, got, "float32")
+    assert v.ok, (bits, m, v)
+
+
 @pytest.mark.parametrize("d_out", [1, 3, 15, 17, 1000])
 def test_d_out_not_divisible_by_the_row_tile(d_out):
     x, q, s, b = draw_qmv(d_out, 512, 4, 2, seed=d_out)
