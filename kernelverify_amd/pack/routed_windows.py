@@ -38,9 +38,9 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "eb04bc55fe54bccff95e7f7c81aaefb00614d998f85b0ae2dc56cfeaa70f6cfa"
+RECORDING_SHA256 = "522f2ff740fe540e08857528ebab21dea0f0654847d28ce448660ae8d55fce02"
 
-KERNEL_SOURCE_SHA256 = "c51b09e4f8373e9a494d480835e451273cbc39536dffabf83a25d13d6a504117"
+KERNEL_SOURCE_SHA256 = "342e2fcd68997e6bad009e0a2f61a0dd2765bf3407903f0539aa6330e61d08d8"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
 
@@ -50,10 +50,16 @@ def rows_per_wave(m: int, bits: int, d_out: int, d_in: int) -> int:
     return ROWS_PER_WAVE[m]
 
 # Cells measured WIN but not routed, with the reason. A window only admits
-# cells contiguous with its lower part; these won at M = 8, where the launch
-# switches to more row tiles per block, above measured losses at M = 6-7
-# (lm_head 4-bit) and M = 5-7 (gate/up 8-bit): islands, not window edges.
-EXCLUDED_CELLS = MappingProxyType({(4, 151936, 2560): frozenset({8}),
+# cells contiguous with its lower part. These won at M = 8, where the launch
+# switches to 16-row block diagonals of two groups, above measured losses or
+# undecided cells at M = 5-7 (2- and 8-bit gate/up, 3- and 4-bit lm_head,
+# 3-bit gate/up); and 2-bit 4096 x 4096 won at M = 6 by 0.4% between two
+# REFUSED cells: islands, not window edges.
+EXCLUDED_CELLS = MappingProxyType({(2, 9728, 2560): frozenset({8}),
+                                   (2, 4096, 4096): frozenset({6}),
+                                   (3, 9728, 2560): frozenset({8}),
+                                   (3, 151936, 2560): frozenset({8}),
+                                   (4, 151936, 2560): frozenset({8}),
                                    (8, 9728, 2560): frozenset({8})})
 
 
