@@ -340,3 +340,19 @@ def test_one_workspace_serves_calls_of_every_shape():
                                         nv[i:i + 1], [t], bits, dtype="float32")
             v = judge(got[i:i + 1], ref, tols[0])
             assert v.ok, (b, h, bits, i, v)
+
+
+def test_32k_target_shape_4bit():
+    """The 32k target: B1, 32 query heads over 8 KV heads, DH 128, 4-bit K/V
+    over T = 32768 cached positions, judged in full against the oracle."""
+    rng = np.random.default_rng(32)
+    b, h, hkv, t, dh, bits = 1, 32, 8, 32768, 128, 4
+    kc, vc = baseline_cache(rng, b, hkv, t, dh)
+    q = rng.standard_normal((b, h, dh)).astype(np.float16)
+    nk = rng.standard_normal((b, hkv, dh)).astype(np.float16)
+    nv = rng.standard_normal((b, hkv, dh)).astype(np.float16)
+    out = run(q, kc[0], vc[0], nk, nv, bits)
+    ref, tols = kv_per_sequence(q, kc, vc, nk, nv, [t], bits)
+    v = judge(out, ref, max(tols))
+    print("32k", v)
+    assert v.ok, v
