@@ -539,6 +539,29 @@ def blas_threads() -> int:
 ISSUE_FILE = ROOT / "profiles" / "issue_counts_bench.json"
 
 
+def trace_steps(steps: int, replays: int = 3) -> int:
+    """The program the kernel-trace profile runs: every row's step captured
+    ``steps`` times back to back in one HIP graph with no event nodes (the
+    profiler does not follow event-record nodes), replayed ``replays``
+    times, so each kernel runs as it does inside the timed region."""
+    from kernelverify_amd import hip
+
+    stream = hip.Stream()
+    for make in row_factories():
+        w = make()
+        w.step(stream)
+        stream.synchronize()
+        g = hip.Graph(stream, lambda: [w.step(stream) for _ in range(steps)])
+        for _ in range(replays):
+            g.launch()
+        stream.synchronize()
+        g.destroy()
+        log(f"[trace] {w.name}: {replays} x {steps} steps")
+        del w
+    print(json.dumps({"trace_steps": steps, "replays": replays}), flush=True)
+    return 0
+
+
 def issue_profile(steps: int) -> int:
     """The program the instruction-count passes profile: every row's step
     ``steps`` times between tag launches (kernelverify_amd/counters.py reads
@@ -614,6 +637,8 @@ def main() -> int:
                     help="skip the other BASELINE qmv configs (configs 1 and 2 beside the headline)")
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline qmv workload (profiling runs)")
+    ap.add_argument("--trace-steps", type=int, default=0, metavar="K",
+                    help="kernel-trace program: every row's step K times in a graph, then exit")
     ap.add_argument("--issue-profile", type=int, default=0, metavar="S",
                     help="run every row S times between tag launches, for rocprofv3 counter "
                          "passes (kernelverify_amd/counters.py); no timing")
@@ -632,6 +657,8 @@ def main() -> int:
     lib.load()
     if args.issue_profile:
         return issue_profile(args.issue_profile)
+    if args.trace_steps:
+        return trace_steps(args.trace_steps)
 
     head = row_factories()[0]()
     log(f"[bench] {head.name}: {len(head.copies)} artefact copies, "

@@ -38,9 +38,9 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "522f2ff740fe540e08857528ebab21dea0f0654847d28ce448660ae8d55fce02"
+RECORDING_SHA256 = "810cf3769bc085d94e303a4247ec8b2218a6a70b243d482857f3199b58a020ab"
 
-KERNEL_SOURCE_SHA256 = "342e2fcd68997e6bad009e0a2f61a0dd2765bf3407903f0539aa6330e61d08d8"
+KERNEL_SOURCE_SHA256 = "5961911427f7f0abf3a97de52d48da3dbbec4ff9cc500c6c312ab82cd80ae324"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
 

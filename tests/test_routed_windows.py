@@ -31,7 +31,7 @@ EXPECTED_TABLE = {
     (4, 1024, 2560): range(1, 9), (4, 2560, 4096): range(1, 9), (4, 2560, 9728): range(1, 12),
     (4, 4096, 2560): range(1, 9), (4, 4096, 4096): range(1, 9), (4, 4096, 14336): range(1, 17),
     (4, 9728, 2560): range(1, 9), (4, 14336, 4096): range(1, 9), (4, 151936, 2560): range(1, 6),
-    (8, 1024, 2560): range(1, 9), (8, 2560, 4096): range(1, 8), (8, 2560, 9728): range(1, 12),
+    (8, 1024, 2560): range(1, 9), (8, 2560, 4096): range(1, 9), (8, 2560, 9728): range(1, 12),
     (8, 4096, 2560): range(1, 9), (8, 4096, 4096): range(1, 9), (8, 4096, 14336): range(1, 17),
     (8, 9728, 2560): range(1, 5), (8, 14336, 4096): range(1, 9), (8, 151936, 2560): range(1, 5),
 }
