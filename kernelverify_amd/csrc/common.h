@@ -77,6 +77,21 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(f16, h);
 }
 
+// fp16 scales and biases loaded ahead of use (16-bit buffer loads into
+// 32-bit registers) are converted by one instruction that reads only the low
+// half, written as such: through a 16-bit type the compiler either masks the
+// loaded register or packs two of them into one, right after the loads,
+// which makes the wave wait for those loads (and every load issued before
+// them) long before the values are used.
+__device__ __forceinline__ uint16_t buffer_load_h16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+__device__ __forceinline__ float h16_to_f32(uint16_t v) {
+  float f;
+  asm("v_cvt_f32_f16 %0, %1" : "=v"(f) : "v"(v));
+  return f;
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 
 

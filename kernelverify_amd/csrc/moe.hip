@@ -250,7 +250,7 @@ struct ExpertArgs {
   // launch routes every token itself (the logits-door contract) instead of
   // reading idx; block (0, 0) also writes the routing to out_idx / out_gate.
   const float* logits;     // [n][n_experts] fp32, or null
-  int n_tokens, epl;       // tokens; experts per lane (1, 2 or 4)
+  int n_tokens, epl;       // tokens (any in-block routing); experts per lane (1, 2 or 4)
   uint32_t* out_idx;       // [n][k]
   float* out_gate;         // [n][k]
   int32_t* t_offsets;      // [E+1]: entries e and e + 1 of every routed e
@@ -625,14 +625,20 @@ constexpr int kEGroupSlots = 9;                      // 8 operand slots + 1 pad 
 template <int BITS, bool SWIGLU>
 struct ExpertStep {
   uint32_t w[SWIGLU ? 2 : 1][MfmaShape<BITS, kEMT>::kWPL];
-  uint32_t s[SWIGLU ? 2 : 1], b[SWIGLU ? 2 : 1];
+  uint16_t s[SWIGLU ? 2 : 1], b[SWIGLU ? 2 : 1];  // fp16 bits of the group scale and bias
 };
 
 // KQ waves share one tile's steps (KQ = 4: one tile per block, for long
 // rows) or each wave runs all of its own tile's steps (KQ = 1: four tiles per
 // block share one staging of the activations, for short rows).
+// At 4 bits, waves per SIMD held at what the register budget of each form
+// allows (three for one tile per wave, four for four waves per tile): the
+// allocator otherwise spends a few registers more and drops one. 8-bit
+// forms need more registers than that and keep the allocator's choice.
 template <int BITS, bool SWIGLU, bool F32IN, int KQ, bool ROUTE = false>
-__global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(kBlock)
+__attribute__((amdgpu_waves_per_eu(BITS == 4 ? (KQ == 1 ? 3 : 4) : 1)))
+void expert_mfma_kernel(ExpertArgs a) {
   using S = MfmaShape<BITS, kEMT>;
   constexpr int NP = SWIGLU ? 2 : 1;            // projections per tile
   constexpr int TPP = F32IN ? kEMT / 2 : kEMT;  // tokens per pass
@@ -642,6 +648,24 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
   __shared__ float red[kWaves][NP][kEMT][16];
   static_assert(!ROUTE || (SWIGLU && !F32IN), "in-block routing is the gate/up launch's");
   const int act = blockIdx.y;
+  const int G = a.d_in / 64;  // a multiple of 4 (checked by the launcher)
+  // In-block routing, up to kEMT tokens (every expert's pairs fit one pass):
+  // thread t requests group t % G of token t / G before routing, so the
+  // activations arrive while the block routes, and stages them right after
+  // it (the pairs' tokens are then known), before the expert's weight loads
+  // go out; otherwise they would return behind the weights.
+  const bool pre_x = ROUTE && a.n_tokens <= kEMT && a.n_tokens * G <= kBlock;  // one pass
+  const int x_tok = pre_x && (int)threadIdx.x < a.n_tokens * G ? (int)threadIdx.x / G : -1;
+  const int x_g = pre_x ? (int)threadIdx.x % G : 0;
+  u32x4 xv[8];
+  if constexpr (ROUTE) {
+    if (x_tok >= 0) {
+      const uint32_t* src =
+          reinterpret_cast<const uint32_t*>(a.x + (size_t)x_tok * a.d_in + x_g * 64);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xv[q] = *reinterpret_cast<const u32x4*>(src + 4 * q);
+    }
+  }
   int e, p0, p1;
   const int32_t* seg = nullptr;  // ROUTE: the expert's flat pair indices (LDS)
   if constexpr (ROUTE) {
@@ -657,7 +681,6 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
     p0 = a.offsets[e];
     p1 = a.offsets[e + 1];
   }
-  const int G = a.d_in / 64;                 // a multiple of 4 (checked by the launcher)
   const int steps = G / S::kNB;
   const int m_stride = G * kEGroupSlots + 1;  // slots per A row
   uint4* xs = lds;
@@ -700,12 +723,48 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr[pj], co + 4 * i, 0, 0);
         R.w[pj][i] = v.x; R.w[pj][i + 1] = v.y; R.w[pj][i + 2] = v.z; R.w[pj][i + 3] = v.w;
       }
-      R.s[pj] = __builtin_amdgcn_raw_buffer_load_b16(sr[pj], so, 0, 0);
-      R.b[pj] = __builtin_amdgcn_raw_buffer_load_b16(br[pj], so, 0, 0);
+      R.s[pj] = buffer_load_h16(sr[pj], so);
+      R.b[pj] = buffer_load_h16(br[pj], so);
     }
   };
   // A wave's steps are kq, kq + KQ, ...; RS of them are in flight at a time
   // (the first RS are requested before anything else).
+  const int nt0 = min(TPP, p1 - p0);
+  if (pre_x) {  // the one pass, q0 = p0
+    // The activations pass through an empty asm here, so no work on them
+    // is scheduled before routing (which would wait for them first, then
+    // for the logits, one memory round trip after the other).
+#pragma unroll
+    for (int q = 0; q < 8; ++q) asm volatile("" : "+v"(xv[q]));
+    // Rows past the expert's pairs are zeros; row m < nt0 is its pair's
+    // token, written by the thread holding that token's group.
+    for (int it = threadIdx.x; it < kEMT * G; it += kBlock) {
+      const int m = it / G, g = it - m * G;
+      if (m >= nt0) {
+        uint4* dst = xs + m * m_stride + g * kEGroupSlots;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[q] = uint4{0, 0, 0, 0};
+        sums[g * kEMT + m] = 0.0f;
+      }
+    }
+    if (x_tok >= 0) {
+      u32x4 ow[8];
+      float sum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        ow[q] = to_slot_order<BITS>(xv[q]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sum = dot2(ow[q][j], 0x3C003C00u, sum);
+      }
+      for (int m = 0; m < nt0; ++m) {
+        if (seg[m] / a.k != x_tok) continue;
+        uint4* dst = xs + m * m_stride + x_g * kEGroupSlots;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[q] = uint4{ow[q].x, ow[q].y, ow[q].z, ow[q].w};
+        sums[x_g * kEMT + m] = sum;
+      }
+    }
+  }
   const int spw = (steps - kq + KQ - 1) / KQ;  // wave-uniform
   ExpertStep<BITS, SWIGLU> R[RS];
 #pragma unroll
@@ -715,7 +774,9 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
 
   for (int q0 = p0; q0 < p1; q0 += TPP) {  // block-uniform passes over the expert's pairs
     const int nt = min(TPP, p1 - q0);
-    if constexpr (!F32IN) {
+    if (pre_x) {
+      // staged before the weight loads (above)
+    } else if constexpr (!F32IN) {
       // Stage: item (token row m, group g), one thread each.
       for (int it = threadIdx.x; it < kEMT * G; it += kBlock) {
         const int m = it / G, g = it - m * G;
@@ -808,8 +869,8 @@ __global__ __launch_bounds__(kBlock) void expert_mfma_kernel(ExpertArgs a) {
         for (int t = 0; t < S::kT; ++t)
           d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_src[t]),
                                                      code_operand<BITS>(Rs.w[pj], t), d, 0, 0, 0);
-        const float sc = f16_bits_to_f32((uint16_t)Rs.s[pj]) * 16777216.0f;  // c * 2^-24
-        const float bi = f16_bits_to_f32((uint16_t)Rs.b[pj]);
+        const float sc = h16_to_f32(Rs.s[pj]) * 16777216.0f;  // c * 2^-24
+        const float bi = h16_to_f32(Rs.b[pj]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[pj][r] = fmaf(sc * mu[r], d[r], fmaf(bi, sm[r], acc[pj][r]));
       }
@@ -960,8 +1021,8 @@ __global__ __launch_bounds__(64 * kDcWaves) void down_combine_kernel(DownCombine
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, co + 4 * i, 0, 0);
         Rs.w[0][i] = v.x; Rs.w[0][i + 1] = v.y; Rs.w[0][i + 2] = v.z; Rs.w[0][i + 3] = v.w;
       }
-      Rs.s[0] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
-      Rs.b[0] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+      Rs.s[0] = buffer_load_h16(sr, so);
+      Rs.b[0] = buffer_load_h16(br, so);
     };
 #pragma unroll
     for (int j = 0; j < RS; ++j) load(R[j], j);
@@ -1040,8 +1101,8 @@ __global__ __launch_bounds__(64 * kDcWaves) void down_combine_kernel(DownCombine
             d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a_src[tt]),
                                                        code_operand<BITS>(R[j].w[0], tt), d, 0, 0,
                                                        0);
-          const float sc = f16_bits_to_f32((uint16_t)R[j].s[0]) * 16777216.0f;  // c * 2^-24
-          const float bi = f16_bits_to_f32((uint16_t)R[j].b[0]);
+          const float sc = h16_to_f32(R[j].s[0]) * 16777216.0f;  // c * 2^-24
+          const float bi = h16_to_f32(R[j].b[0]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc * mu[r], d[r], fmaf(bi, sm[r], acc[r]));
         }
@@ -1429,9 +1490,9 @@ int swiglu_impl(const char* who, const float* logits, const void* x, uint32_t* i
   a.d_out = d_ffn;
   if (route_in_block) {
     a.idx = idx;
+    a.n_tokens = n;
     if (logits_in_block) {
       a.logits = logits;
-      a.n_tokens = n;
       a.epl = epl <= 1 ? 1 : (epl <= 2 ? 2 : 4);
       a.out_idx = idx;
       a.out_gate = gate;

@@ -662,7 +662,7 @@ __global__ __launch_bounds__(kBlock) void qmv_stream_kernel(
 template <int BITS, int RW, int UPL>
 struct PersistSet {
   uint32_t w[UPL][RW][Geom<BITS>::kUnitWords];
-  uint32_t s[UPL][RW], b[UPL][RW];  // fp16 bits of the unit's group scale and bias
+  uint16_t s[UPL][RW], b[UPL][RW];  // fp16 bits of the unit's group scale and bias
 };
 
 template <int BITS, int RW, int UPL, int PD, typename OutT>
@@ -703,8 +703,8 @@ __global__ __launch_bounds__(kBlock) void qmv_persist_kernel(
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, co, 0, 0);
         R.w[j][r][0] = v.x; R.w[j][r][1] = v.y; R.w[j][r][2] = v.z; R.w[j][r][3] = v.w;
         const uint32_t so = ok ? ((uint32_t)row * groups + u / kUnitsPerGroup) * 2 : kOOR;
-        R.s[j][r] = __builtin_amdgcn_raw_buffer_load_b16(sr, so, 0, 0);
-        R.b[j][r] = __builtin_amdgcn_raw_buffer_load_b16(br, so, 0, 0);
+        R.s[j][r] = buffer_load_h16(sr, so);
+        R.b[j][r] = buffer_load_h16(br, so);
       }
     }
   };
@@ -754,8 +754,8 @@ __global__ __launch_bounds__(kBlock) void qmv_persist_kernel(
           unit_dot<BITS, 1, RW>(ring[p].w[j], xp[j], G::kSlotPairs, d);
 #pragma unroll
           for (int r = 0; r < RW; ++r)
-            acc[r] = fmaf(f16_bits_to_f32((uint16_t)ring[p].s[j][r]), d[r][0],
-                          fmaf(f16_bits_to_f32((uint16_t)ring[p].b[j][r]), xsum[j], acc[r]));
+            acc[r] = fmaf(h16_to_f32(ring[p].s[j][r]), d[r][0],
+                          fmaf(h16_to_f32(ring[p].b[j][r]), xsum[j], acc[r]));
         }
         load(ring[p], set + PD * n_waves);
 #pragma unroll

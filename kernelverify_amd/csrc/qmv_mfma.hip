@@ -41,7 +41,7 @@ constexpr int kMfmaStageBytes = 96 * 1024;
 template <int BITS, int MT>
 struct MfmaStep {
   uint32_t w[MfmaShape<BITS, MT>::kWPL];
-  uint32_t s, b;  // fp16 bits of this lane's group scale and bias (zero when out of range)
+  uint16_t s, b;  // fp16 bits of this lane's group scale and bias (zero out of range)
 };
 
 // Staging of x[m][groups g0 .. g0 + kc) in operand order, with the fp32 sum
@@ -171,8 +171,8 @@ __global__ __launch_bounds__(64 * TB * KQ) void qmv_mfma_kernel(
         R.w[i] = v.x; R.w[i + 1] = v.y; R.w[i + 2] = v.z; R.w[i + 3] = v.w;
       }
     }
-    R.s = __builtin_amdgcn_raw_buffer_load_b16(sr, sbo, 0, 0);
-    R.b = __builtin_amdgcn_raw_buffer_load_b16(br, sbo, 0, 0);
+    R.s = buffer_load_h16(sr, sbo);
+    R.b = buffer_load_h16(br, sbo);
   };
 
   u32x4 xv[8];
@@ -205,8 +205,8 @@ __global__ __launch_bounds__(64 * TB * KQ) void qmv_mfma_kernel(
           }
           // D rows 4h + r of this lane: x rows m = (4h + r) % MT of block blk.
           const f32x4 sums = *reinterpret_cast<const f32x4*>(sum_base + rel * 16);
-          const float sc = f16_bits_to_f32((uint16_t)ring[u].s) * 16777216.0f;  // c * 2^-24
-          const float bi = f16_bits_to_f32((uint16_t)ring[u].b);
+          const float sc = h16_to_f32(ring[u].s) * 16777216.0f;  // c * 2^-24
+          const float bi = h16_to_f32(ring[u].b);
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc, d[r], fmaf(bi, sums[r], acc[r]));
         }
