@@ -187,6 +187,8 @@ LEADING_READ_SHAPES = [
     {"threads": 512, "blocks": 1024, "unroll": 1, "load": "non-temporal", "tiles": "strided"},
     {"threads": 256, "blocks": 2048, "unroll": 2, "load": "non-temporal", "tiles": "strided"},
     {"threads": 512, "blocks": 256, "unroll": 16, "load": "non-temporal", "tiles": "strided"},
+    {"threads": 512, "blocks": 1024, "unroll": 2, "load": "non-temporal", "tiles": "contiguous"},
+    {"threads": 1024, "blocks": 256, "unroll": 2, "load": "non-temporal", "tiles": "contiguous"},
 ]
 
 COMPUTE_KINDS = {0: "fp32 FMA (v_fma_f32)", 1: "fp16 dot2 (v_dot2_f32_f16)",
