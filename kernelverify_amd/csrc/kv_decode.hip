@@ -637,12 +637,17 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
   float* xw = xbuf[wave];
   auto xaddr = [](int pos, int g, int h) { return pos * kXS + (pos / 8) * 8 + g * kHp + h; };
 
-  // The slice's cache loads do not wait for the length: they cover the
-  // slice within t_stride (every block of the grid starts inside it), the
-  // length load travels beside them, and positions at or past T are masked
-  // out of the softmax (their scores are -inf, so p = 0 and they add
-  // nothing). Only a block wholly past its sequence's end wastes its first
-  // step's loads.
+  // With one sequence the slice's first cache loads do not wait for the
+  // length: they cover the slice within t_stride (every block of the grid
+  // starts inside it), the length load travels beside them, and positions
+  // at or past T are masked out of the softmax (their scores are -inf, so
+  // p = 0 and they add nothing). Only a block wholly past the sequence's end
+  // wastes them. With several sequences of different lengths such blocks
+  // are common (config 4: 11.7 MB of 120 MB fetched, 1.108 x the algorithmic
+  // bytes), so there the loads wait for the length and stop at it (measured:
+  // config 4 45.2 -> 44.2 us; one sequence 32k 16.17 -> 16.72 us without the
+  // early loads).
+  const bool early = gridDim.z == 1;  // grid-uniform
   const int n_max = min(a.chunk, a.t_stride - slice0);
   SliceRsrc rs;
   {
@@ -686,13 +691,14 @@ __global__ __launch_bounds__(kBlock) void kv_mfma_split_kernel(KvArgs a) {
     }
   }
 
-  if (wave * kP < n_max) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
+  if (early && wave * kP < n_max) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
   const int T = min(max(a.t_cached[b], 0), a.t_stride);
   if (slice0 >= T) {  // block-uniform
     if (c == 0) write_new_entry<DH, G>(a, b, hk);
     return;
   }
   const int n = min(a.chunk, T - slice0);
+  if (!early && wave * kP < n) load_step<BITS, DH, G>(RA, rs, kP * wave, lane);
   const int nsteps = (n + kP - 1) / kP;
   auto step_pos = [&](int t) { return t < nsteps ? kP * t : a.chunk + kP; };
 

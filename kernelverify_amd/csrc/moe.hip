@@ -631,19 +631,23 @@ struct ExpertStep {
 // KQ waves share one tile's steps (KQ = 4: one tile per block, for long
 // rows) or each wave runs all of its own tile's steps (KQ = 1: four tiles per
 // block share one staging of the activations, for short rows).
-// At 4 bits, waves per SIMD held at what the register budget of each form
-// allows (three for one tile per wave, four for four waves per tile): the
-// allocator otherwise spends a few registers more and drops one. 8-bit
+// At 4 bits, four waves per SIMD in both forms: the allocator otherwise
+// spends a few registers more and drops one. With KQ = 1 that is what two
+// steps in flight allow (four took 168 registers, three waves: at n = 32
+// only 768 of the gate/up launch's 1320 live blocks then ran at once, and
+// the rest started as a second generation); each slot is refilled with the
+// step two ahead as soon as it is used, so two stay in flight throughout
+// (measured, config 5 n = 32 107.8 -> 104.6 us, n = 8 53.6 -> 53.2). 8-bit
 // forms need more registers than that and keep the allocator's choice.
 template <int BITS, bool SWIGLU, bool F32IN, int KQ, bool ROUTE = false>
 __global__ __launch_bounds__(kBlock)
-__attribute__((amdgpu_waves_per_eu(BITS == 4 ? (KQ == 1 ? 3 : 4) : 1)))
+__attribute__((amdgpu_waves_per_eu(BITS == 4 ? 4 : 1)))
 void expert_mfma_kernel(ExpertArgs a) {
   using S = MfmaShape<BITS, kEMT>;
   constexpr int NP = SWIGLU ? 2 : 1;            // projections per tile
   constexpr int TPP = F32IN ? kEMT / 2 : kEMT;  // tokens per pass
   constexpr int TB = kWaves / KQ;               // tiles per block
-  constexpr int RS = KQ == 1 ? 4 : 2;           // steps in flight per wave
+  constexpr int RS = 2;                         // steps in flight per wave
   extern __shared__ __align__(16) uint4 lds[];
   __shared__ float red[kWaves][NP][kEMT][16];
   static_assert(!ROUTE || (SWIGLU && !F32IN), "in-block routing is the gate/up launch's");
@@ -875,15 +879,33 @@ void expert_mfma_kernel(ExpertArgs a) {
         for (int r = 0; r < 4; ++r) acc[pj][r] = fmaf(sc * mu[r], d[r], fmaf(bi, sm[r], acc[pj][r]));
       }
     };
-    for (int jb = 0; jb < spw; jb += RS) {  // wave-uniform
-      if (!fresh) {
+    if constexpr (KQ == 1) {
+      // Rolling: slot j is refilled with the step RS ahead right after its
+      // use; after its last use in a pass, with the next pass's step j (the
+      // first RS steps are requested before the first pass).
+      const bool more = q0 + TPP < p1;  // block-uniform: another pass follows
+      for (int jb = 0; jb < spw; jb += RS) {  // wave-uniform
 #pragma unroll
-        for (int j = 0; j < RS; ++j) load(R[j], kq + KQ * (jb + j));
+        for (int j = 0; j < RS; ++j) {
+          if (jb + j < spw) {
+            step(R[j], jb + j);
+            const int nx = jb + j + RS;
+            load(R[j], nx < spw ? nx : (more ? j : steps));  // steps: nothing (reads zeros)
+          }
+        }
       }
-      fresh = false;
+    } else {
+      // Batches of RS steps per wave, requested together.
+      for (int jb = 0; jb < spw; jb += RS) {  // wave-uniform
+        if (!fresh) {
 #pragma unroll
-      for (int j = 0; j < RS; ++j)
-        if (jb + j < spw) step(R[j], kq + KQ * (jb + j));
+          for (int j = 0; j < RS; ++j) load(R[j], kq + KQ * (jb + j));
+        }
+        fresh = false;
+#pragma unroll
+        for (int j = 0; j < RS; ++j)
+          if (jb + j < spw) step(R[j], kq + KQ * (jb + j));
+      }
     }
     // Merge the four row blocks (other groups, same A rows), then the waves.
 #pragma unroll
