@@ -647,7 +647,12 @@ void expert_mfma_kernel(ExpertArgs a) {
   constexpr int NP = SWIGLU ? 2 : 1;            // projections per tile
   constexpr int TPP = F32IN ? kEMT / 2 : kEMT;  // tokens per pass
   constexpr int TB = kWaves / KQ;               // tiles per block
-  constexpr int RS = 2;                         // steps in flight per wave
+  // Steps in flight per wave. The one-tile-per-wave down projection holds
+  // four: a tile of up to four steps (d_in <= 1024) then stays in registers
+  // over all of its expert's passes (two tokens each) instead of streaming
+  // once per pass (config 5 n = 32: down traffic 1.24 x its weights; 103.4
+  // -> 101.3 us).
+  constexpr int RS = (KQ == 1 && F32IN) ? 4 : 2;
   extern __shared__ __align__(16) uint4 lds[];
   __shared__ float red[kWaves][NP][kEMT][16];
   static_assert(!ROUTE || (SWIGLU && !F32IN), "in-block routing is the gate/up launch's");
@@ -753,13 +758,17 @@ void expert_mfma_kernel(ExpertArgs a) {
     }
     if (x_tok >= 0) {
       u32x4 ow[8];
-      float sum = 0.0f;
+      float s0 = 0.0f, s1 = 0.0f;  // the two halves' sums, as the staging loop forms them
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         ow[q] = to_slot_order<BITS>(xv[q]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sum = dot2(ow[q][j], 0x3C003C00u, sum);
+        for (int j = 0; j < 4; ++j) {
+          if (q < 4) s0 = dot2(ow[q][j], 0x3C003C00u, s0);
+          else s1 = dot2(ow[q][j], 0x3C003C00u, s1);
+        }
       }
+      const float sum = s0 + s1;
       for (int m = 0; m < nt0; ++m) {
         if (seg[m] / a.k != x_tok) continue;
         uint4* dst = xs + m * m_stride + x_g * kEGroupSlots;
@@ -781,27 +790,32 @@ void expert_mfma_kernel(ExpertArgs a) {
     if (pre_x) {
       // staged before the weight loads (above)
     } else if constexpr (!F32IN) {
-      // Stage: item (token row m, group g), one thread each.
-      for (int it = threadIdx.x; it < kEMT * G; it += kBlock) {
+      // Stage: item (token row m, group g) in two halves of 32 values on
+      // adjacent lanes (every thread busy, half the registers; n = 32 102.4
+      // -> 100.9 us); the group's sum is the two half sums added.
+      for (int it2 = threadIdx.x; it2 < 2 * kEMT * G; it2 += kBlock) {
+        const int it = it2 >> 1, hf = it2 & 1;
         const int m = it / G, g = it - m * G;
-        uint4* dst = xs + m * m_stride + g * kEGroupSlots;
+        uint4* dst = xs + m * m_stride + g * kEGroupSlots + 4 * hf;
         float sum = 0.0f;
-        u32x4 v[8];
+        u32x4 v[4];
         const bool live = m < nt;
         const int pair = live ? (ROUTE ? seg[q0 - p0 + m] : a.perm[q0 + m]) : 0;
         const int tok = pair / a.k;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.x + (size_t)tok * a.d_in + g * 64);
+        const uint32_t* src =
+            reinterpret_cast<const uint32_t*>(a.x + (size_t)tok * a.d_in + g * 64) + 16 * hf;
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
+        for (int q = 0; q < 4; ++q)
           v[q] = live ? *reinterpret_cast<const u32x4*>(src + 4 * q) : u32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
+        for (int q = 0; q < 4; ++q) {
           const u32x4 ow = to_slot_order<BITS>(v[q]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) sum = dot2(ow[j], 0x3C003C00u, sum);
           dst[q] = uint4{ow.x, ow.y, ow.z, ow.w};
         }
-        sums[g * kEMT + m] = sum;
+        sum += __shfl_xor(sum, 1);  // both lanes of an item take this iteration
+        if (hf == 0) sums[g * kEMT + m] = sum;
       }
     } else {
       // Stage: item (token, group, quarter of 16 values), four lanes per
@@ -882,7 +896,8 @@ void expert_mfma_kernel(ExpertArgs a) {
     if constexpr (KQ == 1) {
       // Rolling: slot j is refilled with the step RS ahead right after its
       // use; after its last use in a pass, with the next pass's step j (the
-      // first RS steps are requested before the first pass).
+      // first RS steps are requested before the first pass). With spw <= RS
+      // every step keeps its slot from pass to pass.
       const bool more = q0 + TPP < p1;  // block-uniform: another pass follows
       for (int jb = 0; jb < spw; jb += RS) {  // wave-uniform
 #pragma unroll
@@ -890,7 +905,8 @@ void expert_mfma_kernel(ExpertArgs a) {
           if (jb + j < spw) {
             step(R[j], jb + j);
             const int nx = jb + j + RS;
-            load(R[j], nx < spw ? nx : (more ? j : steps));  // steps: nothing (reads zeros)
+            if (nx < spw) load(R[j], nx);
+            else if (more && spw > RS) load(R[j], j);
           }
         }
       }
