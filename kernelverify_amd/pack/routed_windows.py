@@ -38,9 +38,9 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "98523e76d2605782dc6c409fbdba944db1fde1aa8e8c03f0fc096faaa242581b"
+RECORDING_SHA256 = "082c01223f66a94a24f7e265b59148b9946f6632286f123cf0556da65f50af7b"
 
-KERNEL_SOURCE_SHA256 = "2378d56925903313b0951830e4379e457dc8b10f63bda7d874386493e7d7929d"
+KERNEL_SOURCE_SHA256 = "f91a0e130f54b035a261529d38a7c2c751f273a987f1380120406a59816e47fd"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
 
@@ -51,16 +51,14 @@ def rows_per_wave(m: int, bits: int, d_out: int, d_in: int) -> int:
 
 # Cells measured WIN but not routed, with the reason. A window only admits
 # cells contiguous with its lower part. These won at M = 8, where the launch
-# switches to 16-row block diagonals of two groups, above measured losses or
-# undecided cells at M = 5-7 (2- and 8-bit gate/up, 3- and 4-bit lm_head,
-# 3-bit gate/up); and 2-bit 4096 x 4096 won at M = 6-7 by under 2% above a
-# REFUSED cell at M = 5: islands, not window edges.
+# switches to 16-row block diagonals of two groups, above measured losses at
+# M = 5-7 (2- and 3-bit gate/up and lm_head, 8-bit lm_head): islands, not
+# window edges.
 EXCLUDED_CELLS = MappingProxyType({(2, 9728, 2560): frozenset({8}),
-                                   (2, 4096, 4096): frozenset({6, 7}),
+                                   (2, 151936, 2560): frozenset({8}),
                                    (3, 9728, 2560): frozenset({8}),
                                    (3, 151936, 2560): frozenset({8}),
-                                   (4, 151936, 2560): frozenset({8}),
-                                   (8, 9728, 2560): frozenset({8})})
+                                   (8, 151936, 2560): frozenset({8})})
 
 
 def _load(path: Path = RECORDING_PATH, pinned: str | None = None) -> dict:
