@@ -650,9 +650,11 @@ struct ExpertStep {
 // 17 us faster at n = 32 without the per-step scale loads; with the tile,
 // n = 32 100.4 -> 87.5 us and n = 8 52.4 -> 46.1. The form holds 164
 // registers (three waves per SIMD): at four it spilled, and ran 91.8 us.
+// The fp32-input down projection takes the same tile when its steps fit
+// one batch (G <= 16): written once, it serves every pass (86.3 us).
 template <int BITS, bool SWIGLU, bool F32IN, int KQ, bool ROUTE = false, bool SBX = false>
 __global__ __launch_bounds__(kBlock)
-__attribute__((amdgpu_waves_per_eu(BITS == 4 ? (SBX ? 3 : 4) : 1)))
+__attribute__((amdgpu_waves_per_eu(BITS == 4 ? ((SBX && SWIGLU) ? 3 : 4) : 1)))
 void expert_mfma_kernel(ExpertArgs a) {
   using S = MfmaShape<BITS, kEMT>;
   constexpr int NP = SWIGLU ? 2 : 1;            // projections per tile
@@ -667,7 +669,8 @@ void expert_mfma_kernel(ExpertArgs a) {
   extern __shared__ __align__(16) uint4 lds[];
   __shared__ float red[kWaves][NP][kEMT][16];
   static_assert(!ROUTE || (SWIGLU && !F32IN), "in-block routing is the gate/up launch's");
-  static_assert(!SBX || (SWIGLU && !F32IN && KQ == 1 && RS == 2), "scale tiles: gate/up, one wave per tile");
+  static_assert(!SBX || (KQ == 1 && (SWIGLU ? (!F32IN && RS == 2) : (F32IN && RS == 4))),
+                "scale tiles: one wave per tile (gate/up, or the fp32-input down projection)");
   const int act = blockIdx.y;
   const int G = a.d_in / 64;  // a multiple of 4 (checked by the launcher)
   // In-block routing, up to kEMT tokens (every expert's pairs fit one pass):
@@ -946,7 +949,7 @@ void expert_mfma_kernel(ExpertArgs a) {
         for (int r = 0; r < 4; ++r) acc[pj][r] = fmaf(sc * mu[r], d[r], fmaf(bi, sm[r], acc[pj][r]));
       }
     };
-    if constexpr (SBX) {
+    if constexpr (SBX && SWIGLU) {
       // Batches of four steps (spw % 4 == 0): the batch's scale tile goes to
       // LDS, the next batch's (or the next pass's first) is requested, then
       // the four steps run with rolling refills of the two step slots.
@@ -968,6 +971,9 @@ void expert_mfma_kernel(ExpertArgs a) {
       // use; after its last use in a pass, with the next pass's step j (the
       // first RS steps are requested before the first pass). With spw <= RS
       // every step keeps its slot from pass to pass.
+      if constexpr (SBX) {  // down projection (spw <= 4): its scale tile once, kept in LDS
+        if (q0 == p0) sbx_commit();
+      }
       const bool more = q0 + TPP < p1;  // block-uniform: another pass follows
       for (int jb = 0; jb < spw; jb += RS) {  // wave-uniform
 #pragma unroll
@@ -1353,9 +1359,11 @@ int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f3
       const int kq = tuning(kTuneMoeKq, (G / 4 <= 4 || max_active >= 32) ? 1 : 4);
       const bool short_rows = kq == 1;
       const dim3 grid(short_rows ? (tiles + 3) / 4 : tiles, max_active);
-      // Gate/up with one tile per wave and whole four-step scale batches
-      // takes the per-wave LDS scale tiles (2560 bytes a wave).
-      const bool sbx = short_rows && swiglu_f16 && !f32_input && G % 16 == 0;
+      // One tile per wave takes the per-wave LDS scale tiles (2560 bytes a
+      // wave): gate/up with whole four-step batches, and the fp32-input down
+      // projection when its tile is one batch kept over every pass (G <= 16;
+      // config 5 n = 32 87.6 -> 86.3 us).
+      const bool sbx = short_rows && ((swiglu_f16 && !f32_input && G % 16 == 0) || (f32_input && G <= 16));
       const size_t lds = ((size_t)kEMT * (G * kEGroupSlots + 1) + 8) * 16 + (size_t)G * kEMT * 8 +
                          (sbx ? (size_t)kWaves * 4 * 16 * 40 : 0);
 #define KVP_EXPERT(SW, F32, KQ, RT)                                                           \
@@ -1365,7 +1373,8 @@ int launch_experts(const ExpertArgs& a, int max_active, bool swiglu_f16, bool f3
       if (route && !(swiglu_f16 && !f32_input))
         return set_error(KVP_INVALID, "kvp_moe: in-block routing is for the gate/up launch");
       if (f32_input) {
-        if (short_rows) KVP_EXPERT(false, true, 1, false); else KVP_EXPERT(false, true, 4, false);
+        if (sbx) hipLaunchKernelGGL((expert_mfma_kernel<BITS, false, true, 1, false, true>), grid, dim3(kBlock), lds, st, a);
+        else if (short_rows) KVP_EXPERT(false, true, 1, false); else KVP_EXPERT(false, true, 4, false);
       } else if (swiglu_f16 && route) {
         if (sbx) KVP_EXPERT_SBX(true);
         else if (short_rows) KVP_EXPERT(true, false, 1, true); else KVP_EXPERT(true, false, 4, true);
