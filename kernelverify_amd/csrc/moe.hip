@@ -765,7 +765,9 @@ void expert_mfma_kernel(ExpertArgs a) {
   uint32_t sxc[NP][2][2];
   auto sbx_load = [&](int st0) {
     if constexpr (SBX) {
-      const uint32_t so = sbx_base + (uint32_t)st0 * 8;
+      // A lane whose step lies past the row's last (a tile of fewer than
+      // four steps) loads nothing.
+      const uint32_t so = st0 + h < steps ? sbx_base + (uint32_t)st0 * 8 : kOutOfRange;
 #pragma unroll
       for (int pj = 0; pj < NP; ++pj) {
         const u32x2 s = __builtin_amdgcn_raw_buffer_load_b64(sr[pj], so, 0, 0);
