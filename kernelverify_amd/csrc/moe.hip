@@ -1419,10 +1419,12 @@ int launch_experts_bits(int bits, const ExpertArgs& a, int max_active, bool swig
 // Tokens up to which the SwiGLU call fuses the down projection with the
 // gated sum (tuning key moe_down_combine overrides): every token then reads
 // its own experts' down tiles. Measured on MI355X, config 5 (128 experts,
-// top-8, 2048 / 768, 4-bit), fused against the down launch + scatter:
-// n = 1 21.2 / 23.9 us, 2 24.3 / 27.9, 4 37.1 / 41.2, 8 55.8 / 57.6, and
-// 32 140.3 / 111.0 (the repeated expert reads then dominate).
-constexpr int kDownCombineTokens = 8;
+// top-8, 2048 / 768, 4-bit), whole call with the fused launch against the
+// down launch (weights held over its passes, scale tiles) + scatter:
+// n = 1 16.5 / 19.0 us, 2 19.2 / 23.4, 4 27.2 / 30.3, 5 36.4 / 37.4,
+// 6 37.6 / 39.1, 7 45.3 / 43.8, 8 45.9 / 45.5, 12 64.6 / 59.2 (the repeated
+// expert reads then dominate).
+constexpr int kDownCombineTokens = 6;
 
 int launch_down_combine(int bits, int out_dtype, const DownCombineArgs& c, int n,
                         hipStream_t st) {
