@@ -236,6 +236,26 @@ def test_config5_many_tokens(n):
     assert v.ok, v
 
 
+@pytest.mark.parametrize("n,e,d_model,d_ffn,constant", [
+    (10, 16, 1024, 768, True),    # gate/up G = 16 (one scale batch), 3 passes; down tile kept over 5
+    (32, 64, 2048, 256, False),   # gate/up G = 32 (two batches a pass), experts past four pairs
+])
+def test_scale_tiles_over_several_passes(n, e, d_model, d_ffn, constant):
+    """The per-wave scale tiles (one tile per wave: gate/up with whole
+    four-step batches, the fp32-input down projection kept over its passes)
+    on experts that take several passes: every pass re-requests the first
+    batch of scales (gate/up) or reuses the tile written in the first (down).
+    Three tokens judged in full against the oracle."""
+    logits = np.zeros((n, e), dtype=np.float32) if constant else None
+    x, mats, logits = swiglu_case(n, e, d_model, d_ffn, 4, seed=120 + n, logits=logits)
+    idx, gate = moe.route(logits, 8)
+    per_expert = np.bincount(idx.ravel().astype(np.int64), minlength=e)
+    assert per_expert.max() > 4  # some expert takes a second gate/up pass
+    out = run_swiglu(x, mats, idx, gate, 4, "float32")
+    v = judge_swiglu(x, mats, idx.astype(np.int64), gate, out, [0, n // 2, n - 1], "float32")
+    assert v.ok, v
+
+
 def test_experts_shared_by_many_tokens():
     """Constant logits send all ten tokens to experts 0..7: each expert runs
     three token groups (four, four, two) over one weight stream."""
