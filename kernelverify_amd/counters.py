@@ -38,6 +38,8 @@ import sys
 from collections import defaultdict
 from pathlib import Path
 
+from kernelverify_amd import build
+
 OPEN_TAG = "probe_fma_kernel"
 CLOSE_TAG = "probe_dot2_kernel"
 TAG_BLOCK = 256  # threads per block of the tag kernels
@@ -48,13 +50,15 @@ AVERAGED = {"OccupancyPercent", "VALUBusy", "MfmaUtil", "VALUUtilization",
 
 
 def library_source_sha256() -> str:
-    """sha256 over every libkvpack source (csrc/*.hip and *.h, by name): the
-    kernels whose instructions a set of counts describes."""
+    """sha256 over every libkvpack source (csrc/*.hip and *.h, by name) and
+    the device flags: the kernels whose instructions a set of counts
+    describes."""
     csrc = Path(__file__).resolve().parent / "csrc"
     h = hashlib.sha256()
     for f in sorted(list(csrc.glob("*.hip")) + list(csrc.glob("*.h"))):
         h.update(f.name.encode())
         h.update(f.read_bytes())
+    h.update(build.flags_fingerprint())
     return h.hexdigest()
 
 

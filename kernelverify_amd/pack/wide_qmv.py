@@ -26,7 +26,7 @@ from pathlib import Path
 
 import numpy as np
 
-from kernelverify_amd import lib
+from kernelverify_amd import build, lib
 from kernelverify_amd.hip import DeviceArray
 from kernelverify_amd.pack.codes import pack_codes, pack_nibbles, unpack_codes  # noqa: F401
 
@@ -51,11 +51,13 @@ KERNEL_SOURCES = ("csrc/qmv.hip", "csrc/qmv_core.h", "csrc/qmv_mfma.hip", "csrc/
 
 
 def kernel_source_sha256() -> str:
-    """sha256 over the qmv kernel sources (the body a routing recording
-    priced; the reference pins the MSL string, routed_windows.py:61-64)."""
+    """sha256 over the qmv kernel sources and the device flags they are
+    compiled with (the body a routing recording priced; the reference pins
+    the MSL string, routed_windows.py:61-64)."""
     h = hashlib.sha256()
     for rel in KERNEL_SOURCES:
         h.update((Path(__file__).resolve().parents[1] / rel).read_bytes())
+    h.update(build.flags_fingerprint())
     return h.hexdigest()
 
 

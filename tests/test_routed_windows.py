@@ -23,11 +23,11 @@ from tests.gates.price_qmv_boundary import classify
 # the matrix cores from M = 2 or 3), less the excluded islands.
 EXPECTED_TABLE = {
     (2, 1024, 2560): range(1, 5), (2, 2560, 4096): range(1, 5), (2, 2560, 9728): range(1, 12),
-    (2, 4096, 2560): range(1, 5), (2, 4096, 4096): range(1, 8), (2, 4096, 14336): range(1, 17),
+    (2, 4096, 2560): range(1, 6), (2, 4096, 4096): range(1, 9), (2, 4096, 14336): range(1, 17),
     (2, 9728, 2560): range(1, 5), (2, 14336, 4096): range(1, 9), (2, 151936, 2560): range(1, 5),
-    (3, 1024, 2560): range(1, 5), (3, 2560, 4096): range(1, 5), (3, 2560, 9728): range(1, 12),
-    (3, 4096, 2560): range(1, 9), (3, 4096, 4096): range(1, 8), (3, 4096, 14336): range(1, 17),
-    (3, 9728, 2560): range(1, 7), (3, 14336, 4096): range(1, 9), (3, 151936, 2560): range(1, 5),
+    (3, 1024, 2560): range(1, 8), (3, 2560, 4096): range(1, 5), (3, 2560, 9728): range(1, 12),
+    (3, 4096, 2560): range(1, 9), (3, 4096, 4096): range(1, 9), (3, 4096, 14336): range(1, 17),
+    (3, 9728, 2560): range(1, 9), (3, 14336, 4096): range(1, 9), (3, 151936, 2560): range(1, 5),
     (4, 1024, 2560): range(1, 9), (4, 2560, 4096): range(1, 9), (4, 2560, 9728): range(1, 12),
     (4, 4096, 2560): range(1, 9), (4, 4096, 4096): range(1, 9), (4, 4096, 14336): range(1, 17),
     (4, 9728, 2560): range(1, 9), (4, 14336, 4096): range(1, 9), (4, 151936, 2560): range(1, 9),
