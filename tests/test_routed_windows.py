@@ -68,6 +68,22 @@ def test_pins_match_the_live_kernel_and_launch_config():
                     m, bits, d_out, d_in), (bits, d_out, d_in, m)
 
 
+def test_a_changed_device_flag_voids_the_pins(monkeypatch):
+    """The digests cover how the kernels are compiled, not only their text:
+    a flag that changes the machine code changes both pins, while include
+    paths (which differ between machines) do not enter them."""
+    from kernelverify_amd import build, counters
+    kernel, library = wide_qmv.kernel_source_sha256(), counters.library_source_sha256()
+    flags = list(build.DEVICE_FLAGS)
+    monkeypatch.setattr(build, "DEVICE_FLAGS", [f for f in flags if not f.startswith("-I")]
+                        + ["-I/elsewhere/include"])
+    assert wide_qmv.kernel_source_sha256() == kernel
+    assert counters.library_source_sha256() == library
+    monkeypatch.setattr(build, "DEVICE_FLAGS", flags + ["-mllvm", "-amdgpu-kernarg-preload-count=0"])
+    assert wide_qmv.kernel_source_sha256() != kernel
+    assert counters.library_source_sha256() != library
+
+
 def test_the_recording_is_read_only_as_its_pinned_bytes(tmp_path):
     changed = tmp_path / rw.RECORDING_PATH.name
     changed.write_bytes(rw.RECORDING_PATH.read_bytes() + b" ")
