@@ -25,7 +25,7 @@ EXPECTED_TABLE = {
     (2, 1024, 2560): range(1, 5), (2, 2560, 4096): range(1, 5), (2, 2560, 9728): range(1, 12),
     (2, 4096, 2560): range(1, 6), (2, 4096, 4096): range(1, 9), (2, 4096, 14336): range(1, 17),
     (2, 9728, 2560): range(1, 5), (2, 14336, 4096): range(1, 9), (2, 151936, 2560): range(1, 5),
-    (3, 1024, 2560): range(1, 8), (3, 2560, 4096): range(1, 5), (3, 2560, 9728): range(1, 12),
+    (3, 1024, 2560): range(1, 9), (3, 2560, 4096): range(1, 5), (3, 2560, 9728): range(1, 12),
     (3, 4096, 2560): range(1, 9), (3, 4096, 4096): range(1, 9), (3, 4096, 14336): range(1, 17),
     (3, 9728, 2560): range(1, 9), (3, 14336, 4096): range(1, 9), (3, 151936, 2560): range(1, 5),
     (4, 1024, 2560): range(1, 9), (4, 2560, 4096): range(1, 9), (4, 2560, 9728): range(1, 12),
@@ -33,7 +33,7 @@ EXPECTED_TABLE = {
     (4, 9728, 2560): range(1, 9), (4, 14336, 4096): range(1, 9), (4, 151936, 2560): range(1, 9),
     (8, 1024, 2560): range(1, 9), (8, 2560, 4096): range(1, 9), (8, 2560, 9728): range(1, 12),
     (8, 4096, 2560): range(1, 9), (8, 4096, 4096): range(1, 9), (8, 4096, 14336): range(1, 17),
-    (8, 9728, 2560): range(1, 9), (8, 14336, 4096): range(1, 9), (8, 151936, 2560): range(1, 6),
+    (8, 9728, 2560): range(1, 9), (8, 14336, 4096): range(1, 9), (8, 151936, 2560): range(1, 9),
 }
 
 
@@ -122,7 +122,8 @@ def test_should_dispatch_reads_the_windows():
     assert wide_qmv.should_dispatch(8, 4, 14336, 4096)
     assert not wide_qmv.should_dispatch(16, 4, 14336, 4096)   # measured LOSS
     assert wide_qmv.should_dispatch(8, 4, 151936, 2560)       # measured WIN, in the window
-    assert not wide_qmv.should_dispatch(8, 8, 151936, 2560)   # measured WIN, excluded island
+    assert wide_qmv.should_dispatch(8, 8, 151936, 2560)       # measured WIN, in the window
+    assert not wide_qmv.should_dispatch(7, 3, 151936, 2560)   # measured WIN, excluded island
     assert not wide_qmv.should_dispatch(1, 4, 14336, 4097)    # never priced
     assert not wide_qmv.should_dispatch(1, 5, 14336, 4096)    # unpriced width
     with pytest.raises(TypeError):
