@@ -369,19 +369,20 @@ int launch_tiles(const void* x, const uint32_t* wq, const void* s, const void* b
                  int m, int d_out, int d_in, hipStream_t st) {
   // More tiles per block share one x staging (less staging per weight
   // byte) but leave fewer blocks. Measured on MI355X (4-bit, with the scale
-  // tiles): four tiles for 768 to 4095 tiles and from 512 at M >= 6
-  // (9728x2560 M = 6: 8.34 against 9.95 us on one), but two from M = 11 at 4
+  // tiles): four tiles for 768 to 4095 tiles and from 512 at M >= 5
+  // (9728x2560 M = 6: 8.34 against 9.95 us on one, M = 5: 8.24 against
+  // 9.67; at 2, 3 and 8 bits too), but two from M = 11 at 4
   // and 8 bits with d_in >= 4096 (14336x4096 M = 12: 33.1 against 37.5 us;
   // M = 9-10 and 2-bit M = 12 lose 4-6% there, and 9728x2560 keeps four:
-  // 19.3 against 21.8); for 4096 tiles and more two at M = 6-8 and four
-  // above (151936x2560 M = 6: 69.8 against 84.2 us on one, M = 16: 184
-  // against 227 on two); else one tile with eight waves on it to keep loads
-  // in flight.
+  // 19.3 against 21.8); for 4096 tiles and more two at M = 5-8 and four
+  // above (151936x2560 M = 6: 69.8 against 84.2 us on one, M = 5: 68.0
+  // against 81.0, at every width; M = 16: 184 against 227 on two); else one
+  // tile with eight waves on it to keep loads in flight.
   const int tiles = (d_out + 15) / 16;
   int pick = 1;
   if (tiles >= 4096) {
-    if (m >= 6) pick = m > 8 ? 4 : 2;
-  } else if (tiles >= 768 || (tiles >= 512 && m >= 6)) {
+    if (m >= 5) pick = m > 8 ? 4 : 2;
+  } else if (tiles >= 768 || (tiles >= 512 && m >= 5)) {
     pick = (BITS >= 4 && m > 10 && d_in >= 4096) ? 2 : 4;
   }
   const int v = tuning(kTuneQmvMfmaTiles, pick);

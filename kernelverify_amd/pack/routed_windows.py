@@ -38,9 +38,9 @@ from types import MappingProxyType
 
 RECORDING_PATH = Path(__file__).resolve().parent / "recordings" / "qmv-boundary-pricing-mi355x.json"
 
-RECORDING_SHA256 = "e7a7bfec9369b6fff7192e3714b817f42f8cc4ba8e3dcaed30edbc2959a032b1"
+RECORDING_SHA256 = "43d6d8319016d9c21c7c62e39814875b2c51e655dedb12956ad0a3245d198f47"
 
-KERNEL_SOURCE_SHA256 = "b9196a5d16175695cfd4107ad3556335b61d06b5ac16902a36bc78fb9f355509"
+KERNEL_SOURCE_SHA256 = "c76bffa3f639c2decd6d9368ee004ca621424f6bbda8ad245185f1c1e9b54e50"
 
 ROWS_PER_WAVE = MappingProxyType({m: (2 if m <= 8 else 1) for m in range(1, 17)})
 
@@ -50,13 +50,10 @@ def rows_per_wave(m: int, bits: int, d_out: int, d_in: int) -> int:
     return ROWS_PER_WAVE[m]
 
 # Cells measured WIN but not routed, with the reason. A window only admits
-# cells contiguous with its lower part. These won at M = 6-8, where the
-# launch puts two or four 16-row tiles in a block, above a measured loss at
-# M = 5 on one tile (2-bit gate/up, 2- and 3-bit lm_head): islands, not
-# window edges.
-EXCLUDED_CELLS = MappingProxyType({(2, 9728, 2560): frozenset({6, 7, 8}),
-                                   (2, 151936, 2560): frozenset({6, 7, 8}),
-                                   (3, 151936, 2560): frozenset({6, 7, 8})})
+# cells contiguous with its lower part: a WIN above a measured LOSS is an
+# island, not a window edge, and is listed here as {(bits, d_out, d_in):
+# frozenset of M}. This recording has none (every window is contiguous).
+EXCLUDED_CELLS = MappingProxyType({})
 
 
 def _load(path: Path = RECORDING_PATH, pinned: str | None = None) -> dict:

@@ -20,14 +20,14 @@ from tests.gates.price_qmv_boundary import classify
 # Written out by hand from kernelverify_amd/pack/recordings/
 # qmv-boundary-pricing-mi355x.json: the tile widths at which kvp_qmv beat the
 # vendor fp16 GEMM with the whole ratio interval above 1 (every width runs on
-# the matrix cores from M = 2 or 3), less the excluded islands.
+# the matrix cores from M = 2 or 3), less any excluded islands (none in this recording).
 EXPECTED_TABLE = {
     (2, 1024, 2560): range(1, 5), (2, 2560, 4096): range(1, 5), (2, 2560, 9728): range(1, 12),
     (2, 4096, 2560): range(1, 6), (2, 4096, 4096): range(1, 9), (2, 4096, 14336): range(1, 17),
-    (2, 9728, 2560): range(1, 5), (2, 14336, 4096): range(1, 9), (2, 151936, 2560): range(1, 5),
-    (3, 1024, 2560): range(1, 9), (3, 2560, 4096): range(1, 5), (3, 2560, 9728): range(1, 12),
+    (2, 9728, 2560): range(1, 9), (2, 14336, 4096): range(1, 9), (2, 151936, 2560): range(1, 9),
+    (3, 1024, 2560): range(1, 8), (3, 2560, 4096): range(1, 5), (3, 2560, 9728): range(1, 12),
     (3, 4096, 2560): range(1, 9), (3, 4096, 4096): range(1, 9), (3, 4096, 14336): range(1, 17),
-    (3, 9728, 2560): range(1, 9), (3, 14336, 4096): range(1, 9), (3, 151936, 2560): range(1, 5),
+    (3, 9728, 2560): range(1, 9), (3, 14336, 4096): range(1, 9), (3, 151936, 2560): range(1, 9),
     (4, 1024, 2560): range(1, 9), (4, 2560, 4096): range(1, 9), (4, 2560, 9728): range(1, 12),
     (4, 4096, 2560): range(1, 9), (4, 4096, 4096): range(1, 9), (4, 4096, 14336): range(1, 17),
     (4, 9728, 2560): range(1, 9), (4, 14336, 4096): range(1, 9), (4, 151936, 2560): range(1, 9),
@@ -123,7 +123,8 @@ def test_should_dispatch_reads_the_windows():
     assert not wide_qmv.should_dispatch(16, 4, 14336, 4096)   # measured LOSS
     assert wide_qmv.should_dispatch(8, 4, 151936, 2560)       # measured WIN, in the window
     assert wide_qmv.should_dispatch(8, 8, 151936, 2560)       # measured WIN, in the window
-    assert not wide_qmv.should_dispatch(7, 3, 151936, 2560)   # measured WIN, excluded island
+    assert wide_qmv.should_dispatch(5, 2, 9728, 2560)         # measured WIN, in the window
+    assert not wide_qmv.should_dispatch(8, 3, 1024, 2560)     # measured LOSS
     assert not wide_qmv.should_dispatch(1, 4, 14336, 4097)    # never priced
     assert not wide_qmv.should_dispatch(1, 5, 14336, 4096)    # unpriced width
     with pytest.raises(TypeError):
